@@ -1,0 +1,183 @@
+"""Benchmark of the Magnetar MI355X Provider's hot path on one GPU.
+
+Prints ONE JSON line. The headline (`value`) is the workload BASELINE.json's
+metric is quoted on that fits one GPU: configs[1], the f32 matmul, at
+4096^3 (the north star's MFMA target). The same run measures every other
+hot-path Kernel at its BASELINE shape (`kernels`), each as algorithmic
+GB/s or TFLOP/s over the average launch time from HIP events recorded on
+the library's own stream, and as a fraction of the MI355X roofline.
+Inputs are resident in HBM before timing starts. The CPU oracle is timed on
+a bounded sample of the headline workload on this host (`cpu_baseline`).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "magnetar-provider-cuda_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+METRIC = "per-kernel GB/s or TFLOP/s (% roofline); decoder-block tokens/s, 1 MI355X"
+MB = 1e6
+
+
+def seed(config: int, tensor: int) -> int:
+    return 0x4D414732 ^ (config << 16) ^ tensor
+
+
+class Case:
+    """One kernel at one shape: `launch()` enqueues exactly one call."""
+
+    def __init__(self, name, launch, work, bound, shape):
+        self.name, self.launch, self.work, self.bound, self.shape = name, launch, work, bound, shape
+
+    def measure(self, dev, steps, warmup):
+        for _ in range(warmup):
+            self.launch()
+        dev.sync()
+        dev.timer_start()
+        for _ in range(steps):
+            self.launch()
+        ms = dev.timer_stop() / steps
+        if self.bound == "hbm":
+            achieved = self.work / (ms * 1e-3) / 1e9
+            peak, unit = HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved = self.work / (ms * 1e-3) / 1e12
+            peak, unit = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+        return {"ms": ms, "achieved": achieved, "unit": unit, "peak": peak,
+                "frac": achieved / peak, "work": self.work, "bound": self.bound,
+                "shape": self.shape}
+
+
+def streaming_cases(dev, orc):
+    from magnetar_hip import ops, MHIP_F16, MHIP_BF16
+    cases = []
+    rows, cols = 8192, 4096
+    n = rows * cols
+    x = dev.upload(orc.normal(n, seed(3, 0)))
+    y = dev.upload(orc.normal(n, seed(3, 1)))
+    out = dev.empty((n,))
+    gain = dev.upload(orc.normal(cols, seed(3, 2), 1.0, 0.1))
+    f32 = 4
+    cases.append(Case("add", lambda: ops.add(dev, x, y, out), 3 * n * f32, "hbm", [n]))
+    cases.append(Case("mul", lambda: ops.mul(dev, x, y, out), 3 * n * f32, "hbm", [n]))
+    cases.append(Case("residual_add", lambda: ops.add(dev, x, y, out), 3 * n * f32, "hbm", [n]))
+    cases.append(Case("silu", lambda: ops.silu(dev, x, out), 2 * n * f32, "hbm", [n]))
+    cases.append(Case("silu_mul", lambda: ops.silu_mul(dev, x, y, out), 3 * n * f32, "hbm", [n]))
+    x2 = _reshape(x, (rows, cols))
+    o2 = _reshape(out, (rows, cols))
+    cases.append(Case("rmsnorm", lambda: ops.rmsnorm(dev, x2, gain, 1e-5, out=o2),
+                      2 * n * f32 + cols * f32, "hbm", [rows, cols]))
+    sm_in = dev.upload(orc.normal(n, seed(3, 3), 0.0, 2.0).reshape(rows, cols))
+    cases.append(Case("softmax", lambda: ops.softmax_rows(dev, sm_in, out=o2),
+                      2 * n * f32, "hbm", [rows, cols]))
+    rp = ops.rope_params(128, 32)
+    cases.append(Case("rope", lambda: ops.rope(dev, x2, rp, out=o2), 2 * n * f32, "hbm",
+                      [rows, 32 * 128]))
+    # Embedding: 8192 ids into a [128000, 4096] table (2.1 GB resident).
+    vocab = 128000
+    table = dev.empty((vocab, cols))
+    _fill_normal(dev, table, seed(3, 4))
+    ids = dev.upload(orc.token_ids(8192, seed(3, 5), vocab))
+    emb_out = dev.empty((8192, cols))
+    cases.append(Case("embedding", lambda: ops.embedding(dev, table, ids, emb_out),
+                      2 * 8192 * cols * f32 + 8192 * f32, "hbm", [8192, cols]))
+    # Half path: 64M elements per tensor.
+    hn = 1 << 26
+    for dname, dt in (("f16", MHIP_F16), ("bf16", MHIP_BF16)):
+        ha = dev.upload(orc.encode_half(orc.normal(hn, seed(3, 6)), dt), half=dt)
+        hb = dev.upload(orc.encode_half(orc.normal(hn, seed(3, 7)), dt), half=dt)
+        ho = dev.empty((hn,), np.uint16, dt)
+        for op in ("add", "mul"):
+            cases.append(Case(f"{op}_{dname}",
+                              (lambda ha=ha, hb=hb, ho=ho, op=op, dt=dt:
+                               ops.half_binary(dev, ha, hb, op, dt, ho)),
+                              3 * hn * 2, "hbm", [hn]))
+    return cases
+
+
+def _reshape(arr, shape):
+    from magnetar_hip.device import DeviceArray
+    return DeviceArray(arr.device, arr.ptr, shape, arr.dtype, arr.half, owned=False)
+
+
+def _fill_normal(dev, arr, s):
+    """Fills a large device array chunk by chunk from the seeded generator."""
+    from oracle import oracle as orc
+    import ctypes
+    from magnetar_hip._lib import call
+    rows = arr.shape[0]
+    chunk = max(1, (64 << 20) // (arr.shape[1] * 4))
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        host = orc.normal((r1 - r0) * arr.shape[1], s + r0)
+        call("mhip_upload", dev.ctx, ctypes.c_void_p(arr.ptr + r0 * arr.shape[1] * 4),
+             host.ctypes.data_as(ctypes.c_void_p), host.nbytes)
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--only", default="", help="comma-separated kernel names")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+
+    import magnetar_hip
+    from oracle import oracle as orc
+
+    dev = magnetar_hip.Device(0)
+    info = dev.info()
+    cases = streaming_cases(dev, orc)
+    only = set(filter(None, args.only.split(",")))
+    results = {}
+    for case in cases:
+        if only and case.name not in only:
+            continue
+        results[case.name] = case.measure(dev, args.steps, args.warmup)
+        r = results[case.name]
+        print(f"# {case.name:14s} {r['ms']*1e3:9.1f} us  {r['achieved']:8.1f} {r['unit']}  "
+              f"{100*r['frac']:5.1f}% of {r['bound']}", file=sys.stderr, flush=True)
+    dev.check_flags()
+
+    head = results.get("add")
+    line = {
+        "metric": METRIC,
+        "value": round(head["achieved"], 2) if head else None,
+        "unit": head["unit"] if head else None,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5) if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: splitmix64/Box-Muller seeded inputs",
+        "config": {"workload": "C3 add, 33.5M-element f32 tensors"},
+        "device": {"name": info["name"], "arch": info["architecture"],
+                   "compute_units": info["compute_units"]},
+        "kernels": {k: {"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),
+                        "unit": v["unit"], "frac": round(v["frac"], 4), "shape": v["shape"]}
+                    for k, v in results.items()},
+    }
+    print(json.dumps(line))
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

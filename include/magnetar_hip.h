@@ -1,0 +1,181 @@
+/*
+ * magnetar_hip.h -- the C ABI of the Magnetar MI355X (gfx950) Provider.
+ *
+ * This is the drop-in boundary for the reference's hot path: the f32
+ * required-now Kernel set plus the f16/bf16 add/mul path that the reference
+ * CUDA Provider dispatches from `CudaExecutor::run_invocation_with_offer`
+ * (src/executor.rs:1422-2027) to `CudaKernels` launch wrappers
+ * (src/kernels.rs) over cudarc. Every entry point is plain C: device pointers,
+ * sizes and small POD parameter structs; no C++ or torch types cross it.
+ *
+ * Conventions
+ *  - Every function returns an `mhip_status`. On failure a redacted,
+ *    thread-local diagnostic is available from `mhip_last_error_detail()`
+ *    (never a native pointer or handle; src/error.rs:44-52).
+ *  - Kernel entry points enqueue on the context's single in-order HIP stream
+ *    and return before the device finishes (the reference's one-stream model,
+ *    src/kernels.rs:796-827). `mhip_download` and `mhip_sync` wait.
+ *  - Data-dependent failures (an invalid embedding id, a softmax row with no
+ *    finite entry) are recorded in a device flag word and reported by
+ *    `mhip_check_flags`, which waits; the chained path checks once at the end
+ *    instead of after every call.
+ *  - All f32 tensors are contiguous row-major.
+ */
+#ifndef MAGNETAR_HIP_H
+#define MAGNETAR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error categories: one-to-one with `CudaErrorCode` (src/error.rs:15-42). */
+typedef enum {
+    MHIP_OK = 0,
+    MHIP_SHAPE_UNSUPPORTED = 1,
+    MHIP_DTYPE_UNSUPPORTED = 2,
+    MHIP_LAYOUT_UNSUPPORTED = 3,
+    MHIP_EXECUTION_FAILED = 4,
+    MHIP_OUT_OF_DEVICE_MEMORY = 5,
+    MHIP_COMPILATION_FAILED = 6,
+    MHIP_DRIVER_FAILED = 7,
+    MHIP_DEVICE_UNAVAILABLE = 8,
+    MHIP_CAPTURE_UNSUPPORTED = 9
+} mhip_status;
+
+/* Half-precision storage formats (`CudaHalfDType`, src/kernels.rs:191-251). */
+typedef enum { MHIP_F16 = 0, MHIP_BF16 = 1 } mhip_half_dtype;
+
+typedef struct mhip_ctx mhip_ctx;
+
+/* Device metadata (`cuda_device_descriptor`, src/device.rs:41-74). */
+typedef struct {
+    int ordinal;
+    char name[256];
+    char architecture[64];      /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    uint64_t total_memory;
+    uint64_t free_memory;
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint64_t lds_per_workgroup;
+    int pressure;               /* 0 low, 1 moderate, 2 high, 3 saturated, -1 unknown
+                                   (buckets at free ratio 0.5/0.2/0.05, src/device.rs:81-92) */
+} mhip_device_info;
+
+/* Flag bits reported by mhip_check_flags. */
+#define MHIP_FLAG_EMBEDDING_INVALID_ID 1u
+#define MHIP_FLAG_SOFTMAX_NON_FINITE 2u
+
+/* ---- diagnostics ------------------------------------------------------ */
+const char* mhip_last_error_detail(void);
+const char* mhip_status_name(mhip_status status);
+const char* mhip_version(void);
+
+/* ---- context and device (src/provider.rs:119-179) ---------------------- */
+/* Number of visible HIP devices; 0 (and MHIP_OK) when there is no driver or GPU. */
+mhip_status mhip_device_count(int* count);
+/* Binds device `ordinal`; MHIP_DEVICE_UNAVAILABLE (never a crash) when absent. */
+mhip_status mhip_ctx_create(int ordinal, mhip_ctx** out);
+mhip_status mhip_ctx_destroy(mhip_ctx* ctx);
+mhip_status mhip_device_query(mhip_ctx* ctx, mhip_device_info* info);
+
+/* ---- buffers (CudaDeviceBuffer, src/kernels.rs:253-379, :1630-1665, :2118-2164) */
+mhip_status mhip_alloc(mhip_ctx* ctx, size_t bytes, void** device_ptr);
+mhip_status mhip_free(mhip_ctx* ctx, void* device_ptr);
+mhip_status mhip_upload(mhip_ctx* ctx, void* device_dst, const void* host_src, size_t bytes);
+/* Waits for the stream, then copies. */
+mhip_status mhip_download(mhip_ctx* ctx, void* host_dst, const void* device_src, size_t bytes);
+mhip_status mhip_copy(mhip_ctx* ctx, void* device_dst, const void* device_src, size_t bytes);
+mhip_status mhip_zero(mhip_ctx* ctx, void* device_dst, size_t bytes);
+mhip_status mhip_sync(mhip_ctx* ctx);
+/* Waits, reads and clears the flag word; returns MHIP_SHAPE_UNSUPPORTED for an
+ * invalid embedding id (src/kernels.rs:3984-3997) or MHIP_EXECUTION_FAILED for
+ * a softmax row with no finite entry (src/kernels.rs:4371-4378). `flags` may be
+ * NULL. */
+mhip_status mhip_check_flags(mhip_ctx* ctx, uint32_t* flags);
+
+/* Stream timing with HIP events on the context's stream. */
+mhip_status mhip_timer_start(mhip_ctx* ctx);
+/* Records the stop event, waits for it, returns elapsed milliseconds. */
+mhip_status mhip_timer_stop(mhip_ctx* ctx, float* elapsed_ms);
+
+/* ---- f32 elementwise (src/kernels.rs:2956-3118, :3227-3252, :4492-4523) ---- */
+/* out[i] = a[i] + b[i]                         add_kernel, src/kernels.cu:30-35 */
+mhip_status mhip_add_f32(mhip_ctx* ctx, const float* a, const float* b, float* out, uint64_t n);
+/* out[i] = a[i] + bias[i % cols]; n % cols == 0  bias_add_kernel, src/kernels.cu:1091-1096 */
+mhip_status mhip_bias_add_f32(mhip_ctx* ctx, const float* a, const float* bias, float* out,
+                              uint64_t cols, uint64_t n);
+/* out[i] = a[i] * b[i]                         mul_kernel, src/kernels.cu:55-60 */
+mhip_status mhip_mul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out, uint64_t n);
+/* out[i] = a[i] * b[0]                         mul_scalar_kernel, src/kernels.cu:112-117 */
+mhip_status mhip_mul_scalar_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
+                                uint64_t n);
+/* out[i] = x * (1 / (1 + expf(-x)))            silu_kernel, src/kernels.cu:73-79 */
+mhip_status mhip_silu_f32(mhip_ctx* ctx, const float* x, float* out, uint64_t n);
+/* out[i] = silu(gate[i]) * up[i]               silu_mul_kernel, src/kernels.cu:64-71 */
+mhip_status mhip_silu_mul_f32(mhip_ctx* ctx, const float* gate, const float* up, float* out,
+                              uint64_t n);
+/* out[i] = x[i] * factor                       scale_kernel, src/kernels.cu:95-101 */
+mhip_status mhip_scale_f32(mhip_ctx* ctx, const float* x, float* out, float factor, uint64_t n);
+
+/* ---- half precision on 2-byte buffers (src/kernels.rs:2172-2266, src/kernels.cu:2806-2939) */
+/* out = enc(dec(a) op dec(b)), op in f32, RNE encode; bit-exact. */
+mhip_status mhip_add_half(mhip_ctx* ctx, const uint16_t* a, const uint16_t* b, uint16_t* out,
+                          uint64_t n, mhip_half_dtype dtype);
+mhip_status mhip_mul_half(mhip_ctx* ctx, const uint16_t* a, const uint16_t* b, uint16_t* out,
+                          uint64_t n, mhip_half_dtype dtype);
+/* f32 <-> half on the device: the upload_half / download_half codec
+ * (src/kernels.rs:2172-2219, src/half_precision.rs:14-125) without the host trip. */
+mhip_status mhip_encode_half(mhip_ctx* ctx, const float* in, uint16_t* out, uint64_t n,
+                             mhip_half_dtype dtype);
+mhip_status mhip_decode_half(mhip_ctx* ctx, const uint16_t* in, float* out, uint64_t n,
+                             mhip_half_dtype dtype);
+
+/* ---- embedding gather (src/kernels.rs:3833-3997, src/kernels.cu:127-176) ---- */
+/* out[r, :] = table[ids[r], :] for f32 ids that are in-range non-negative
+ * integers; an invalid id leaves its row unwritten and sets
+ * MHIP_FLAG_EMBEDDING_INVALID_ID. */
+mhip_status mhip_embedding_f32(mhip_ctx* ctx, const float* table, uint64_t vocab, uint64_t dim,
+                               const float* ids, uint64_t num_ids, float* out);
+
+/* ---- row reductions ----------------------------------------------------- */
+/* y = x * (1/sqrtf(mean(x^2) + eps)) * w; `weight` NULL for scale 1;
+ * weight_row_stride 0 (broadcast row) or cols (per-row).
+ * rmsnorm_kernel, src/kernels.cu:1098-1138; src/kernels.rs:4013-4104 */
+mhip_status mhip_rmsnorm_f32(mhip_ctx* ctx, const float* in, const float* weight, float* out,
+                             uint64_t rows, uint64_t cols, uint64_t weight_row_stride,
+                             float eps);
+/* Row softmax; a row whose max is not finite sets MHIP_FLAG_SOFTMAX_NON_FINITE.
+ * softmax_rows_kernel, src/kernels.cu:1232-1260; src/kernels.rs:4357-4386 */
+mhip_status mhip_softmax_rows_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t rows,
+                                  uint64_t cols);
+
+/* ---- RoPE (rope_kernel, src/kernels.cu:1147-1229; src/kernels.rs:4224-4355) ---- */
+typedef struct {
+    float base;                     /* > 0, finite (default 10000) */
+    float scale;                    /* > 0, finite (default 1) */
+    uint64_t dimension;             /* even, <= head width */
+    uint64_t position_offset;
+    uint64_t head_count;            /* divides cols */
+    uint32_t half_split;            /* 0 interleaved (2p, 2p+1); 1 half-split (p, p + dim/2) */
+    uint64_t rotated_pairs;         /* partial rotary: pairs >= this pass through; clamp to dim/2 */
+    float banded_factor;            /* 0 disables banded frequency scaling */
+    float low_freq_factor;
+    float high_freq_factor;
+    float original_context_length;
+    float yarn_factor;              /* 0 disables YaRN */
+    float yarn_low;                 /* YaRN correction range */
+    float yarn_high;
+    float amplitude;                /* YaRN attention factor; 1 otherwise */
+} mhip_rope_params;
+/* Fills `p` with the reference defaults for `dimension` and `head_count`. */
+void mhip_rope_params_default(mhip_rope_params* p, uint64_t dimension, uint64_t head_count);
+mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t rows,
+                          uint64_t cols, const mhip_rope_params* params);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MAGNETAR_HIP_H */

@@ -1,0 +1,50 @@
+// Internal helpers shared by the HIP translation units of libmagnetar_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "magnetar_hip.h"
+
+// One bound device: its stream (all work is ordered on it), the flag word for
+// data-dependent failures and the timing events.
+struct mhip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t* flags = nullptr;  // device word, bits MHIP_FLAG_*
+    hipEvent_t timer_start = nullptr;
+    hipEvent_t timer_stop = nullptr;
+    uint32_t compute_units = 0;
+    // RoPE per-pair (frequency, amplitude) tables already on the device,
+    // keyed by their exact host contents; a decoder reuses one table.
+    struct RopeTable {
+        std::vector<float> host;
+        float* device = nullptr;
+    };
+    std::vector<RopeTable> rope_tables;
+};
+
+namespace mhip {
+
+// Records `detail` as this thread's last error and returns `status`.
+mhip_status fail(mhip_status status, const std::string& detail);
+// Maps a HIP runtime error onto the stable categories (src/error.rs:71-91).
+mhip_status from_hip(hipError_t err, const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// Checks the launch that was just enqueued.
+mhip_status check_launch(const char* what);
+
+}  // namespace mhip
+
+#define MHIP_REQUIRE_CTX(ctx)                                                     \
+    do {                                                                          \
+        if ((ctx) == nullptr)                                                     \
+            return mhip::fail(MHIP_DEVICE_UNAVAILABLE, "no device context");      \
+    } while (0)

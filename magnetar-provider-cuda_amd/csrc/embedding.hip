@@ -1,0 +1,97 @@
+// Embedding gather: out[r, :] = table[ids[r], :].
+//
+// The reference gives one thread per id, each copying its whole row serially
+// (src/kernels.cu:127-176), so neighbouring threads touch addresses `dim`
+// floats apart. Here a group of threads (one wave for rows up to 256
+// vectors, four waves above) copies one row with coalesced dwordx4 loads,
+// all loads issued before the stores. Ids are f32 values (src/kernels.rs:3833-3840);
+// an id is valid iff id >= 0, id == floor(id) and id < vocab. An invalid id
+// leaves its row unwritten and sets MHIP_FLAG_EMBEDDING_INVALID_ID, which
+// mhip_check_flags reports as the reference's ShapeUnsupported failure
+// (src/kernels.rs:3984-3997).
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ bool valid_id(float raw, uint64_t vocab, uint64_t* id) {
+    if (raw < 0.0f || raw != floorf(raw)) return false;  // negative, fractional or NaN
+    if (static_cast<double>(raw) >= static_cast<double>(vocab)) return false;
+    *id = static_cast<uint64_t>(raw);
+    return true;
+}
+
+// TPR threads per row, 256 / TPR rows per workgroup, UNROLL vectors per
+// thread in flight.
+template <int TPR, int UNROLL>
+__global__ __launch_bounds__(kThreads) void embedding_vec_kernel(
+    const float* __restrict__ table, uint64_t vocab, uint64_t dim4, const float* __restrict__ ids,
+    uint64_t num_ids, float* __restrict__ out, uint32_t* flags) {
+    constexpr int kRows = kThreads / TPR;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+    const int lane = threadIdx.x % TPR;
+    if (row >= num_ids) return;
+    uint64_t id = 0;
+    if (!valid_id(ids[row], vocab, &id)) {
+        if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
+        return;
+    }
+    const float4* src = reinterpret_cast<const float4*>(table) + id * dim4;
+    float4* dst = reinterpret_cast<float4*>(out) + row * dim4;
+    for (uint64_t c0 = lane; c0 < dim4; c0 += static_cast<uint64_t>(TPR) * UNROLL) {
+        float4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t c = c0 + static_cast<uint64_t>(u) * TPR;
+            if (c < dim4) v[u] = src[c];
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t c = c0 + static_cast<uint64_t>(u) * TPR;
+            if (c < dim4) dst[c] = v[u];
+        }
+    }
+}
+
+// Any dim or alignment: one wave per row, scalar copies.
+__global__ __launch_bounds__(kThreads) void embedding_scalar_kernel(
+    const float* table, uint64_t vocab, uint64_t dim, const float* ids, uint64_t num_ids,
+    float* out, uint32_t* flags) {
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (row >= num_ids) return;
+    uint64_t id = 0;
+    if (!valid_id(ids[row], vocab, &id)) {
+        if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
+        return;
+    }
+    for (uint64_t c = lane; c < dim; c += 64) out[row * dim + c] = table[id * dim + c];
+}
+
+}  // namespace
+
+extern "C" mhip_status mhip_embedding_f32(mhip_ctx* ctx, const float* table, uint64_t vocab,
+                                          uint64_t dim, const float* ids, uint64_t num_ids,
+                                          float* out) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (num_ids == 0 || dim == 0) return MHIP_OK;
+    if (!table || !ids || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "embedding: null buffer");
+    if (num_ids >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "embedding: too many ids");
+    const bool vec = dim % 4 == 0 && mhip::aligned16(table) && mhip::aligned16(out);
+    const uint64_t dim4 = dim / 4;
+    if (vec && dim4 > 256) {
+        hipLaunchKernelGGL((embedding_vec_kernel<256, 4>), dim3(static_cast<unsigned>(num_ids)),
+                           dim3(kThreads), 0, ctx->stream, table, vocab, dim4, ids, num_ids, out,
+                           ctx->flags);
+    } else if (vec) {
+        hipLaunchKernelGGL((embedding_vec_kernel<64, 4>),
+                           dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads),
+                           0, ctx->stream, table, vocab, dim4, ids, num_ids, out, ctx->flags);
+    } else {
+        hipLaunchKernelGGL(embedding_scalar_kernel,
+                           dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads),
+                           0, ctx->stream, table, vocab, dim, ids, num_ids, out, ctx->flags);
+    }
+    return mhip::check_launch("embedding lookup");
+}

@@ -1,0 +1,279 @@
+// Rotary position embedding.
+//
+// Semantics are `rope_kernel`'s (src/kernels.cu:1147-1229) with the checks
+// of `rope_scaled` (src/kernels.rs:4224-4355): each row holds head_count
+// heads of head_width = cols / head_count columns; in each head the first
+// `dimension` columns rotate in pairs -- interleaved (2p, 2p+1) or half-split
+// (p, p + dimension/2) -- by angle (offset + row) * scale * freq[p]; the
+// other columns pass through.
+//
+// Two things differ from the reference's one-thread-per-pair launch:
+//  - the per-pair frequency (powf, then the banded / YaRN adjustment) depends
+//    on the pair only, so the host computes it once per call with the same
+//    f32 operations and keeps the table on the device; a position of 8191
+//    turns a one-ulp frequency difference into 1e-4 of angle, so this also
+//    makes the angles bit-identical to the CPU oracle's;
+//  - sin/cos depend on (row, pair) only, so one workgroup per row computes
+//    them once into LDS and every head of the row reuses them; the row then
+//    streams through with dwordx4 loads.
+#include "common.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint64_t kMaxHalf = 4096;  // LDS table: 2 x half floats, at most 32 KiB
+
+// The host-side frequency table: the f32 operations of src/kernels.cu:1197-1221.
+void rope_table(const mhip_rope_params& p, std::vector<float>& t) {
+    const uint64_t half = p.dimension / 2;
+    t.assign(2 * half, 0.0f);
+    for (uint64_t pair = 0; pair < half; ++pair) {
+        float frequency = powf(p.base, -2.0f * static_cast<float>(pair) / static_cast<float>(p.dimension));
+        if (p.banded_factor > 0.0f) {
+            float wavelength = 6.283185307179586f / frequency;
+            if (wavelength < p.original_context_length / p.high_freq_factor) {
+                // High frequencies are kept.
+            } else if (wavelength > p.original_context_length / p.low_freq_factor) {
+                frequency = frequency / p.banded_factor;
+            } else {
+                float smooth = (p.original_context_length / wavelength - p.low_freq_factor) /
+                               (p.high_freq_factor - p.low_freq_factor);
+                frequency = (1.0f - smooth) * frequency / p.banded_factor + smooth * frequency;
+            }
+        }
+        if (p.yarn_factor > 0.0f) {
+            float high = p.yarn_low == p.yarn_high ? p.yarn_high + 0.001f : p.yarn_high;
+            float ramp = (static_cast<float>(pair) - p.yarn_low) / (high - p.yarn_low);
+            ramp = fminf(fmaxf(ramp, 0.0f), 1.0f);
+            float interpolated = frequency / p.yarn_factor;
+            frequency = interpolated * ramp + frequency * (1.0f - ramp);
+        }
+        const bool rotated = pair < p.rotated_pairs;
+        t[pair] = rotated ? frequency : 0.0f;
+        t[half + pair] = rotated ? p.amplitude : 1.0f;
+    }
+}
+
+// Returns the device copy of `table`, uploading it on first use.
+mhip_status device_table(mhip_ctx* ctx, const std::vector<float>& table, const float** out) {
+    for (auto& entry : ctx->rope_tables) {
+        if (entry.host.size() == table.size() &&
+            std::memcmp(entry.host.data(), table.data(), table.size() * sizeof(float)) == 0) {
+            *out = entry.device;
+            return MHIP_OK;
+        }
+    }
+    if (ctx->rope_tables.size() >= 16) {
+        // Wait for kernels that may still read the oldest table, then drop it.
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->rope_tables.front().device);
+        ctx->rope_tables.erase(ctx->rope_tables.begin());
+    }
+    mhip_ctx::RopeTable entry;
+    entry.host = table;
+    const size_t bytes = table.size() * sizeof(float);
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&entry.device), bytes ? bytes : 4);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(entry.device, table.data(), bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    if (err != hipSuccess) {
+        if (entry.device) (void)hipFree(entry.device);
+        return mhip::from_hip(err, "uploading the RoPE frequency table");
+    }
+    ctx->rope_tables.push_back(entry);
+    *out = ctx->rope_tables.back().device;
+    return MHIP_OK;
+}
+
+struct RopeArgs {
+    const float* in;
+    float* out;
+    const float* table;  // [half] frequencies then [half] amplitudes
+    uint64_t rows, cols, head_width, dimension, half, position_offset;
+    float scale;
+};
+
+// Fills LDS with (cos, sin) * amplitude for this row's pairs.
+__device__ __forceinline__ void row_sincos(const RopeArgs& a, uint64_t row, float* cs, float* sn) {
+    const float position = static_cast<float>(a.position_offset + row) * a.scale;
+    for (uint64_t p = threadIdx.x; p < a.half; p += kThreads) {
+        const float angle = position * a.table[p];
+        const float amp = a.table[a.half + p];
+        float s, c;
+        sincosf(angle, &s, &c);
+        sn[p] = s * amp;
+        cs[p] = c * amp;
+    }
+}
+
+__device__ __forceinline__ void rotate(float a, float b, float c, float s, float* o1, float* o2) {
+#pragma clang fp contract(off)
+    *o1 = a * c - b * s;
+    *o2 = a * s + b * c;
+}
+
+// Interleaved pairing, vector path: cols, head_width and dimension are
+// multiples of 4, so a dwordx4 at head offset j holds pairs j/2 and j/2+1
+// (both rotated or both passed through).
+__global__ __launch_bounds__(kThreads) void rope_interleaved_vec_kernel(RopeArgs a) {
+    extern __shared__ float lds[];
+    float* cs = lds;
+    float* sn = lds + a.half;
+    const uint64_t row = blockIdx.x;
+    row_sincos(a, row, cs, sn);
+    __syncthreads();
+    const uint64_t cols4 = a.cols / 4, hw4 = a.head_width / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.in) + row * cols4;
+    float4* o4 = reinterpret_cast<float4*>(a.out) + row * cols4;
+    for (uint64_t c = threadIdx.x; c < cols4; c += kThreads) {
+        const uint64_t j = (c % hw4) * 4;
+        float4 v = x4[c];
+        if (j < a.dimension) {
+            const uint64_t p = j / 2;
+            float4 r;
+            rotate(v.x, v.y, cs[p], sn[p], &r.x, &r.y);
+            rotate(v.z, v.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
+            v = r;
+        }
+        o4[c] = v;
+    }
+}
+
+// Half-split pairing, vector path: half is a multiple of 4, so the dwordx4
+// at head offset j < half pairs with the one at j + half.
+__global__ __launch_bounds__(kThreads) void rope_half_split_vec_kernel(RopeArgs a) {
+    extern __shared__ float lds[];
+    float* cs = lds;
+    float* sn = lds + a.half;
+    const uint64_t row = blockIdx.x;
+    row_sincos(a, row, cs, sn);
+    __syncthreads();
+    const uint64_t cols4 = a.cols / 4, hw4 = a.head_width / 4, half4 = a.half / 4;
+    const uint64_t dim4 = a.dimension / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.in) + row * cols4;
+    float4* o4 = reinterpret_cast<float4*>(a.out) + row * cols4;
+    // Per head: half4 rotating slot pairs, then hw4 - dim4 pass-through slots.
+    const uint64_t per_head = half4 + (hw4 - dim4);
+    const uint64_t heads = a.cols / a.head_width;
+    for (uint64_t t = threadIdx.x; t < heads * per_head; t += kThreads) {
+        const uint64_t h = t / per_head, k = t % per_head;
+        const uint64_t base = h * hw4;
+        if (k < half4) {
+            float4 u = x4[base + k], w = x4[base + k + half4];
+            const uint64_t p = k * 4;
+            float4 ru, rw;
+            rotate(u.x, w.x, cs[p], sn[p], &ru.x, &rw.x);
+            rotate(u.y, w.y, cs[p + 1], sn[p + 1], &ru.y, &rw.y);
+            rotate(u.z, w.z, cs[p + 2], sn[p + 2], &ru.z, &rw.z);
+            rotate(u.w, w.w, cs[p + 3], sn[p + 3], &ru.w, &rw.w);
+            o4[base + k] = ru;
+            o4[base + k + half4] = rw;
+        } else {
+            const uint64_t s = base + dim4 + (k - half4);
+            o4[s] = x4[s];
+        }
+    }
+}
+
+// Any shape or alignment: one thread per (head, pair) plus one per
+// pass-through column of the row.
+__global__ __launch_bounds__(kThreads) void rope_scalar_kernel(RopeArgs a, uint32_t half_split) {
+    extern __shared__ float lds[];
+    float* cs = lds;
+    float* sn = lds + a.half;
+    const uint64_t row = blockIdx.x;
+    row_sincos(a, row, cs, sn);
+    __syncthreads();
+    const uint64_t heads = a.cols / a.head_width;
+    const float* x = a.in + row * a.cols;
+    float* o = a.out + row * a.cols;
+    const uint64_t rest = a.head_width - a.dimension;
+    for (uint64_t t = threadIdx.x; t < heads * (a.half + rest); t += kThreads) {
+        const uint64_t h = t / (a.half + rest), k = t % (a.half + rest);
+        const uint64_t base = h * a.head_width;
+        if (k < a.half) {
+            const uint64_t first = half_split ? base + k : base + 2 * k;
+            const uint64_t second = half_split ? base + k + a.half : base + 2 * k + 1;
+            float r1, r2;
+            rotate(x[first], x[second], cs[k], sn[k], &r1, &r2);
+            o[first] = r1;
+            o[second] = r2;
+        } else {
+            const uint64_t col = base + a.dimension + (k - a.half);
+            o[col] = x[col];
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void mhip_rope_params_default(mhip_rope_params* p, uint64_t dimension, uint64_t head_count) {
+    if (!p) return;
+    std::memset(p, 0, sizeof(*p));
+    p->base = 10000.0f;
+    p->scale = 1.0f;
+    p->dimension = dimension;
+    p->head_count = head_count;
+    p->rotated_pairs = dimension / 2;
+    p->amplitude = 1.0f;
+}
+
+mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t rows,
+                          uint64_t cols, const mhip_rope_params* params) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (!params) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rope: null params");
+    mhip_rope_params p = *params;
+    if (p.head_count == 0 || cols % p.head_count != 0)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
+                          "RoPE head_count " + std::to_string(p.head_count) +
+                              " must be positive and evenly divide the row width " +
+                              std::to_string(cols));
+    const uint64_t head_width = cols / p.head_count;
+    if (p.dimension == 0 || p.dimension % 2 != 0 || p.dimension > head_width)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
+                          "RoPE dimension " + std::to_string(p.dimension) +
+                              " must be positive, even, and at most the head width " +
+                              std::to_string(head_width));
+    if (!std::isfinite(p.base) || p.base <= 0.0f)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RoPE base must be finite and positive");
+    if (!std::isfinite(p.scale) || p.scale <= 0.0f)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RoPE scale must be finite and positive");
+    if (p.banded_factor > 0.0f && p.yarn_factor > 0.0f)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
+                          "RoPE takes one frequency scaling, not banded and YaRN together");
+    const uint64_t half = p.dimension / 2;
+    if (half > kMaxHalf)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RoPE dimension exceeds 8192");
+    if (p.rotated_pairs > half) p.rotated_pairs = half;
+    if (rows == 0) return MHIP_OK;
+    if (!in || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rope: null buffer");
+    if (rows >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rope: too many rows");
+    std::vector<float> table;
+    rope_table(p, table);
+    const float* dtable = nullptr;
+    mhip_status st = device_table(ctx, table, &dtable);
+    if (st != MHIP_OK) return st;
+    RopeArgs a{in, out, dtable, rows, cols, head_width, p.dimension, half, p.position_offset,
+               p.scale};
+    const unsigned lds = static_cast<unsigned>(2 * half * sizeof(float));
+    const bool aligned = mhip::aligned16(in) && mhip::aligned16(out) && cols % 4 == 0 &&
+                         head_width % 4 == 0;
+    if (aligned && !p.half_split && p.dimension % 4 == 0) {
+        hipLaunchKernelGGL(rope_interleaved_vec_kernel, dim3(static_cast<unsigned>(rows)),
+                           dim3(kThreads), lds, ctx->stream, a);
+    } else if (aligned && p.half_split && half % 4 == 0) {
+        hipLaunchKernelGGL(rope_half_split_vec_kernel, dim3(static_cast<unsigned>(rows)),
+                           dim3(kThreads), lds, ctx->stream, a);
+    } else {
+        hipLaunchKernelGGL(rope_scalar_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
+                           lds, ctx->stream, a, p.half_split);
+    }
+    return mhip::check_launch("rope");
+}
+
+}  // extern "C"

@@ -1,0 +1,256 @@
+// Row reductions: RMSNorm and row softmax.
+//
+// A row is read from HBM once into registers (VPT dwordx4 vectors per
+// thread), reduced across a group of G threads -- one wave64 (G = 64, four
+// rows per workgroup) for rows up to 1024 floats, one four-wave workgroup
+// (G = 256) up to 16384 floats -- with butterfly shuffles inside each wave
+// and one LDS exchange between waves, then written once. Rows that are
+// longer, not a multiple of 4 or not 16-byte aligned take a looped kernel
+// that re-reads the row from cache.
+//
+// The reference uses one 256-thread block and a shared-memory tree for
+// RMSNorm (src/kernels.cu:1098-1138) and one thread per row for softmax
+// (src/kernels.cu:1232-1260). The results here differ from the CPU oracle's
+// ascending sums only in summation order.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct SumOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+    static constexpr float identity() { return 0.0f; }
+};
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+    static constexpr float identity() { return -INFINITY; }
+};
+
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Reduces over the G threads of this row's group. For G == 256 the four
+// waves meet in `scratch` (4 floats); every thread gets the result.
+template <int G, class Op>
+__device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
+    v = wave_reduce(v, op);
+    if constexpr (G == 256) {
+        const int wave = threadIdx.x / 64;
+        if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+        __syncthreads();
+        v = op(op(scratch[0], scratch[1]), op(scratch[2], scratch[3]));
+        __syncthreads();
+    }
+    return v;
+}
+
+template <int G, int VPT>
+__global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
+    const float* __restrict__ in, const float* __restrict__ weight, float* __restrict__ out,
+    uint64_t rows, uint64_t cols, uint64_t weight_row_stride, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float scratch[4];
+    constexpr int kRowsPerBlock = kThreads / G;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
+    const int lane = threadIdx.x % G;
+    const uint64_t cols4 = cols / 4;
+    const bool live = row < rows;  // G == 256 rows are always live; waves may not be
+    const float4* x4 = reinterpret_cast<const float4*>(in) + row * cols4;
+    float4 x[VPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        uint64_t c = lane + static_cast<uint64_t>(v) * G;
+        x[v] = (live && c < cols4) ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
+    }
+    ss = group_reduce<G>(ss, SumOp{}, scratch);
+    if (!live) return;
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
+    const float4* w4 = weight ? reinterpret_cast<const float4*>(weight + row * weight_row_stride)
+                              : nullptr;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        uint64_t c = lane + static_cast<uint64_t>(v) * G;
+        if (c < cols4) {
+            float4 y;
+            if (w4) {
+                float4 w = w4[c];
+                y = make_float4(x[v].x * inv * w.x, x[v].y * inv * w.y, x[v].z * inv * w.z,
+                                x[v].w * inv * w.w);
+            } else {
+                y = make_float4(x[v].x * inv, x[v].y * inv, x[v].z * inv, x[v].w * inv);
+            }
+            o4[c] = y;
+        }
+    }
+}
+
+template <int G, int VPT>
+__global__ __launch_bounds__(kThreads) void softmax_vec_kernel(const float* __restrict__ in,
+                                                               float* __restrict__ out,
+                                                               uint64_t rows, uint64_t cols,
+                                                               uint32_t* flags) {
+    __shared__ float scratch[4];
+    constexpr int kRowsPerBlock = kThreads / G;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
+    const int lane = threadIdx.x % G;
+    const uint64_t cols4 = cols / 4;
+    const bool live = row < rows;
+    const float4* x4 = reinterpret_cast<const float4*>(in) + row * cols4;
+    float4 x[VPT];
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        uint64_t c = lane + static_cast<uint64_t>(v) * G;
+        x[v] = (live && c < cols4) ? x4[c]
+                                   : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        m = fmaxf(m, fmaxf(fmaxf(x[v].x, x[v].y), fmaxf(x[v].z, x[v].w)));
+    }
+    m = group_reduce<G>(m, MaxOp{}, scratch);
+    // A row with no finite maximum fails the call (src/kernels.rs:4371-4378).
+    const bool bad = !isfinite(m);
+    if (live && bad && lane == 0) atomicOr(flags, MHIP_FLAG_SOFTMAX_NON_FINITE);
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        uint64_t c = lane + static_cast<uint64_t>(v) * G;
+        if (c < cols4 && !bad) {
+            x[v] = make_float4(expf(x[v].x - m), expf(x[v].y - m), expf(x[v].z - m),
+                               expf(x[v].w - m));
+            s += (x[v].x + x[v].y) + (x[v].z + x[v].w);
+        }
+    }
+    s = group_reduce<G>(s, SumOp{}, scratch);
+    if (!live || bad) return;
+    float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        uint64_t c = lane + static_cast<uint64_t>(v) * G;
+        if (c < cols4) o4[c] = make_float4(x[v].x / s, x[v].y / s, x[v].z / s, x[v].w / s);
+    }
+}
+
+// Looped fallbacks: one workgroup per row, any cols and alignment.
+__device__ __forceinline__ float block_reduce_sum(float v, float* scratch) {
+    return group_reduce<256>(v, SumOp{}, scratch);
+}
+
+__global__ __launch_bounds__(kThreads) void rmsnorm_loop_kernel(
+    const float* in, const float* weight, float* out, uint64_t cols, uint64_t weight_row_stride,
+    float eps) {
+#pragma clang fp contract(off)
+    __shared__ float scratch[4];
+    const uint64_t row = blockIdx.x;
+    const float* x = in + row * cols;
+    float ss = 0.0f;
+    for (uint64_t c = threadIdx.x; c < cols; c += kThreads) ss += x[c] * x[c];
+    ss = block_reduce_sum(ss, scratch);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    const float* w = weight ? weight + row * weight_row_stride : nullptr;
+    float* y = out + row * cols;
+    for (uint64_t c = threadIdx.x; c < cols; c += kThreads)
+        y[c] = w ? x[c] * inv * w[c] : x[c] * inv;
+}
+
+__global__ __launch_bounds__(kThreads) void softmax_loop_kernel(const float* in, float* out,
+                                                                uint64_t cols, uint32_t* flags) {
+    __shared__ float scratch[4];
+    const uint64_t row = blockIdx.x;
+    const float* x = in + row * cols;
+    float m = -INFINITY;
+    for (uint64_t c = threadIdx.x; c < cols; c += kThreads) m = fmaxf(m, x[c]);
+    m = group_reduce<256>(m, MaxOp{}, scratch);
+    if (!isfinite(m)) {
+        if (threadIdx.x == 0) atomicOr(flags, MHIP_FLAG_SOFTMAX_NON_FINITE);
+        return;
+    }
+    float s = 0.0f;
+    for (uint64_t c = threadIdx.x; c < cols; c += kThreads) s += expf(x[c] - m);
+    s = block_reduce_sum(s, scratch);
+    float* y = out + row * cols;
+    for (uint64_t c = threadIdx.x; c < cols; c += kThreads) y[c] = expf(x[c] - m) / s;
+}
+
+enum class RowKind { Rms, Softmax };
+
+template <RowKind KIND, int G, int VPT>
+void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
+                uint64_t cols, uint64_t wstride, float eps) {
+    const unsigned blocks = static_cast<unsigned>(mhip::ceil_div(rows, kThreads / G));
+    if constexpr (KIND == RowKind::Rms)
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
+                           ctx->stream, in, weight, out, rows, cols, wstride, eps);
+    else
+        hipLaunchKernelGGL((softmax_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
+                           ctx->stream, in, out, rows, cols, ctx->flags);
+}
+
+// Picks (G, VPT) for a row of cols4 vectors; returns false when the row
+// does not fit the register-resident kernels.
+template <RowKind KIND>
+bool dispatch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
+                  uint64_t cols, uint64_t wstride, float eps) {
+    const uint64_t c4 = cols / 4;
+    if (c4 <= 64) launch_vec<KIND, 64, 1>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 128) launch_vec<KIND, 64, 2>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 256) launch_vec<KIND, 64, 4>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 512) launch_vec<KIND, 256, 2>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 1024) launch_vec<KIND, 256, 4>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 2048) launch_vec<KIND, 256, 8>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else if (c4 <= 4096) launch_vec<KIND, 256, 16>(ctx, rows, in, weight, out, cols, wstride, eps);
+    else return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+mhip_status mhip_rmsnorm_f32(mhip_ctx* ctx, const float* in, const float* weight, float* out,
+                             uint64_t rows, uint64_t cols, uint64_t weight_row_stride,
+                             float eps) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (cols == 0) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RMSNorm hidden dimension is 0");
+    if (!(eps > 0.0f)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RMSNorm epsilon must be positive");
+    if (weight_row_stride != 0 && weight_row_stride != cols)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "RMSNorm weight stride must be 0 or cols");
+    if (rows == 0) return MHIP_OK;
+    if (!in || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rmsnorm: null buffer");
+    if (rows >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rmsnorm: too many rows");
+    const bool vec = cols % 4 == 0 && mhip::aligned16(in) && mhip::aligned16(out) &&
+                     (!weight || mhip::aligned16(weight));
+    if (!(vec && dispatch_vec<RowKind::Rms>(ctx, rows, in, weight, out, cols, weight_row_stride,
+                                             eps)))
+        hipLaunchKernelGGL(rmsnorm_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
+                           0, ctx->stream, in, weight, out, cols, weight_row_stride, eps);
+    return mhip::check_launch("rmsnorm");
+}
+
+mhip_status mhip_softmax_rows_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t rows,
+                                  uint64_t cols) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (rows == 0 || cols == 0) {
+        // Every row of zero columns has max -inf: the reference fails it.
+        if (rows != 0) return mhip::fail(MHIP_EXECUTION_FAILED,
+                                         "softmax has a row with no finite entry to normalize");
+        return MHIP_OK;
+    }
+    if (!in || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "softmax: null buffer");
+    if (rows >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "softmax: too many rows");
+    const bool vec = cols % 4 == 0 && mhip::aligned16(in) && mhip::aligned16(out);
+    if (!(vec && dispatch_vec<RowKind::Softmax>(ctx, rows, in, nullptr, out, cols, 0, 0.0f)))
+        hipLaunchKernelGGL(softmax_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
+                           0, ctx->stream, in, out, cols, ctx->flags);
+    return mhip::check_launch("softmax");
+}
+
+}  // extern "C"

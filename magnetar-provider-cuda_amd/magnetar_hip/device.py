@@ -1,0 +1,141 @@
+"""A bound MI355X device and its device-resident arrays (numpy in, numpy out).
+
+This is the Python view of the C ABI's context and buffer entry points; it
+owns nothing but the handles. Shapes and dtypes ride along with each buffer
+the way `CudaDeviceBuffer` carries its shape (reference src/kernels.rs:253-379).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import MagnetarHipError, call, lib
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    call("mhip_device_count", ctypes.byref(n))
+    return n.value
+
+
+class DeviceArray:
+    """A device allocation with a shape and a numpy dtype (f32, or uint16 for halves)."""
+
+    __slots__ = ("device", "ptr", "shape", "dtype", "nbytes", "half", "_owned", "__weakref__")
+
+    def __init__(self, device: "Device", ptr: int, shape: Sequence[int], dtype, half=None,
+                 owned: bool = True):
+        self.device = device
+        self.ptr = ptr
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.half = half  # None for f32, else _lib.MHIP_F16 / MHIP_BF16
+        self._owned = owned
+
+    @property
+    def size(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def free(self) -> None:
+        if self._owned and self.ptr:
+            lib().mhip_free(self.device.ctx, ctypes.c_void_p(self.ptr))
+        self.ptr = 0
+        self._owned = False
+
+    def __del__(self):
+        try:
+            if self._owned and self.ptr and self.device.ctx:
+                lib().mhip_free(self.device.ctx, ctypes.c_void_p(self.ptr))
+        except Exception:
+            pass
+
+    def numpy(self) -> np.ndarray:
+        return self.device.download(self)
+
+    def __repr__(self):
+        return f"DeviceArray(shape={self.shape}, dtype={self.dtype}, half={self.half})"
+
+
+class Device:
+    """One HIP device context (`mhip_ctx`): a single in-order stream."""
+
+    def __init__(self, ordinal: int = 0):
+        handle = ctypes.c_void_p()
+        call("mhip_ctx_create", ordinal, ctypes.byref(handle))
+        self.ctx = handle
+        self.ordinal = ordinal
+
+    def close(self) -> None:
+        if self.ctx:
+            lib().mhip_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> dict:
+        info = _lib.DeviceInfo()
+        call("mhip_device_query", self.ctx, ctypes.byref(info))
+        return {
+            "ordinal": info.ordinal,
+            "name": info.name.decode(),
+            "architecture": info.architecture.decode(),
+            "total_memory": info.total_memory,
+            "free_memory": info.free_memory,
+            "compute_units": info.compute_units,
+            "wavefront_size": info.wavefront_size,
+            "lds_per_workgroup": info.lds_per_workgroup,
+            "pressure": info.pressure,
+        }
+
+    # ---- buffers ----
+    def empty(self, shape: Sequence[int], dtype=np.float32, half=None) -> DeviceArray:
+        nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize
+        ptr = ctypes.c_void_p()
+        call("mhip_alloc", self.ctx, nbytes, ctypes.byref(ptr))
+        return DeviceArray(self, ptr.value or 0, shape, dtype, half)
+
+    def zeros(self, shape: Sequence[int], dtype=np.float32, half=None) -> DeviceArray:
+        arr = self.empty(shape, dtype, half)
+        call("mhip_zero", self.ctx, ctypes.c_void_p(arr.ptr), arr.nbytes)
+        return arr
+
+    def upload(self, host: np.ndarray, half=None) -> DeviceArray:
+        host = np.ascontiguousarray(host)
+        arr = self.empty(host.shape, host.dtype, half)
+        if arr.nbytes:
+            call("mhip_upload", self.ctx, ctypes.c_void_p(arr.ptr),
+                 host.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
+        return arr
+
+    def download(self, arr: DeviceArray) -> np.ndarray:
+        out = np.empty(arr.shape, dtype=arr.dtype)
+        call("mhip_download", self.ctx, out.ctypes.data_as(ctypes.c_void_p),
+             ctypes.c_void_p(arr.ptr), arr.nbytes)
+        return out
+
+    def sync(self) -> None:
+        call("mhip_sync", self.ctx)
+
+    def check_flags(self) -> int:
+        flags = ctypes.c_uint32(0)
+        call("mhip_check_flags", self.ctx, ctypes.byref(flags))
+        return flags.value
+
+    def timer_start(self) -> None:
+        call("mhip_timer_start", self.ctx)
+
+    def timer_stop(self) -> float:
+        ms = ctypes.c_float(0.0)
+        call("mhip_timer_stop", self.ctx, ctypes.byref(ms))
+        return ms.value
+
+
+__all__ = ["Device", "DeviceArray", "MagnetarHipError", "device_count"]

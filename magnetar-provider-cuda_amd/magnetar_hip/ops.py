@@ -1,0 +1,125 @@
+"""Thin calls of the C ABI's kernel entry points on DeviceArrays.
+
+Each function enqueues one launch on the device's stream and returns the
+output array; nothing waits unless the caller downloads or checks flags.
+Sizes come from the arrays; shape rules beyond element counts belong to the
+executor (the reference's `CudaKernels` layer).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import call
+from .device import Device, DeviceArray
+
+
+def _p(arr: DeviceArray | None):
+    return ctypes.c_void_p(arr.ptr if arr is not None else 0)
+
+
+def _out(dev: Device, out, shape, dtype=np.float32, half=None):
+    return out if out is not None else dev.empty(shape, dtype, half)
+
+
+def add(dev: Device, a: DeviceArray, b: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, a.shape)
+    call("mhip_add_f32", dev.ctx, _p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def bias_add(dev: Device, a: DeviceArray, bias: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, a.shape)
+    call("mhip_bias_add_f32", dev.ctx, _p(a), _p(bias), _p(out), bias.size, a.size)
+    return out
+
+
+def mul(dev: Device, a: DeviceArray, b: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, a.shape)
+    call("mhip_mul_f32", dev.ctx, _p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def mul_scalar(dev: Device, a: DeviceArray, b: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, a.shape)
+    call("mhip_mul_scalar_f32", dev.ctx, _p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def silu(dev: Device, x: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, x.shape)
+    call("mhip_silu_f32", dev.ctx, _p(x), _p(out), x.size)
+    return out
+
+
+def silu_mul(dev: Device, gate: DeviceArray, up: DeviceArray, out=None) -> DeviceArray:
+    out = _out(dev, out, gate.shape)
+    call("mhip_silu_mul_f32", dev.ctx, _p(gate), _p(up), _p(out), gate.size)
+    return out
+
+
+def scale(dev: Device, x: DeviceArray, factor: float, out=None) -> DeviceArray:
+    out = _out(dev, out, x.shape)
+    call("mhip_scale_f32", dev.ctx, _p(x), _p(out), ctypes.c_float(factor), x.size)
+    return out
+
+
+def half_binary(dev: Device, a: DeviceArray, b: DeviceArray, op: str, dtype: int,
+                out=None) -> DeviceArray:
+    out = _out(dev, out, a.shape, np.uint16, dtype)
+    name = "mhip_add_half" if op == "add" else "mhip_mul_half"
+    call(name, dev.ctx, _p(a), _p(b), _p(out), a.size, dtype)
+    return out
+
+
+def encode_half(dev: Device, x: DeviceArray, dtype: int, out=None) -> DeviceArray:
+    out = _out(dev, out, x.shape, np.uint16, dtype)
+    call("mhip_encode_half", dev.ctx, _p(x), _p(out), x.size, dtype)
+    return out
+
+
+def decode_half(dev: Device, x: DeviceArray, dtype: int, out=None) -> DeviceArray:
+    out = _out(dev, out, x.shape)
+    call("mhip_decode_half", dev.ctx, _p(x), _p(out), x.size, dtype)
+    return out
+
+
+def embedding(dev: Device, table: DeviceArray, ids: DeviceArray, out=None) -> DeviceArray:
+    vocab, dim = table.shape
+    out = _out(dev, out, (ids.size, dim))
+    call("mhip_embedding_f32", dev.ctx, _p(table), vocab, dim, _p(ids), ids.size, _p(out))
+    return out
+
+
+def rmsnorm(dev: Device, x: DeviceArray, weight: DeviceArray | None, eps: float,
+            cols: int | None = None, weight_row_stride: int = 0, out=None) -> DeviceArray:
+    cols = cols if cols is not None else x.shape[-1]
+    rows = x.size // cols
+    out = _out(dev, out, x.shape)
+    call("mhip_rmsnorm_f32", dev.ctx, _p(x), _p(weight), _p(out), rows, cols,
+         weight_row_stride, ctypes.c_float(eps))
+    return out
+
+
+def softmax_rows(dev: Device, x: DeviceArray, out=None) -> DeviceArray:
+    rows, cols = x.shape
+    out = _out(dev, out, x.shape)
+    call("mhip_softmax_rows_f32", dev.ctx, _p(x), _p(out), rows, cols)
+    return out
+
+
+def rope_params(dimension: int, head_count: int = 1, **kw) -> _lib.RopeParams:
+    p = _lib.RopeParams()
+    _lib.lib().mhip_rope_params_default(ctypes.byref(p), dimension, head_count)
+    for key, value in kw.items():
+        setattr(p, key, value)
+    return p
+
+
+def rope(dev: Device, x: DeviceArray, params: _lib.RopeParams, out=None) -> DeviceArray:
+    rows, cols = x.shape
+    out = _out(dev, out, x.shape)
+    call("mhip_rope_f32", dev.ctx, _p(x), _p(out), rows, cols, ctypes.byref(params))
+    return out
