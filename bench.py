@@ -28,6 +28,10 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 METRIC = "per-kernel GB/s or TFLOP/s (% roofline); decoder-block tokens/s, 1 MI355X"
 MB = 1e6
+HEADLINE = "matmul_4096"
+# HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
+# scaled by a plain copy's reading); null until measured.
+TRAFFIC: dict = {}
 
 
 def seed(config: int, tensor: int) -> int:
@@ -106,6 +110,41 @@ def streaming_cases(dev, orc):
     return cases
 
 
+def matmul_cases(dev, orc):
+    from magnetar_hip import ops
+    cases = []
+    for size in (1024, 2048, 4096, 8192):
+        a = dev.upload(orc.uniform(size * size, seed(2, size), -1.0, 1.0).reshape(size, size))
+        b = dev.upload(orc.uniform(size * size, seed(2, size + 1), -1.0, 1.0).reshape(size, size))
+        c = dev.empty((size, size))
+        cases.append(Case(f"matmul_{size}", (lambda a=a, b=b, c=c: ops.matmul(dev, a, b, out=c)),
+                          2.0 * size ** 3, "mfma", [size, size, size]))
+    a = dev.upload(orc.uniform(4096, seed(2, 1), -1.0, 1.0).reshape(1, 4096))
+    b = dev.upload(orc.uniform(4096 * 11008, seed(2, 2), -1.0, 1.0).reshape(4096, 11008))
+    c = dev.empty((1, 11008))
+    cases.append(Case("matmul_1x4096x11008", lambda: ops.matmul(dev, a, b, out=c),
+                      4 * (4096 * 11008 + 4096 + 11008), "hbm", [1, 4096, 11008]))
+    return cases
+
+
+def cpu_baseline(orc, budget_s=12.0):
+    """The oracle's matmul (f32, k ascending, one thread) on whole rows of the
+    4096^3 headline product, as many rows as fit the time budget."""
+    size = 4096
+    a = orc.uniform(size * size, seed(2, size), -1.0, 1.0).reshape(size, size)
+    b = orc.uniform(size * size, seed(2, size + 1), -1.0, 1.0).reshape(size, size)
+    rows, t0 = 0, time.perf_counter()
+    step = 4
+    while time.perf_counter() - t0 < budget_s and rows < size:
+        orc.matmul_rows(a, b, rows, rows + step)
+        rows += step
+    elapsed = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * size * size / elapsed / 1e12, 6), "unit": "TFLOP/s",
+            "cores": 1, "kind": "port",
+            "sample": f"{rows} of {size} rows of the {size}^3 f32 product ({elapsed:.1f} s, "
+                      f"oracle/oracle.c orc_matmul_rows, one thread)"}
+
+
 def _reshape(arr, shape):
     from magnetar_hip.device import DeviceArray
     return DeviceArray(arr.device, arr.ptr, shape, arr.dtype, arr.half, owned=False)
@@ -142,7 +181,7 @@ def main(argv=None):
 
     dev = magnetar_hip.Device(0)
     info = dev.info()
-    cases = streaming_cases(dev, orc)
+    cases = matmul_cases(dev, orc) + streaming_cases(dev, orc)
     only = set(filter(None, args.only.split(",")))
     results = {}
     for case in cases:
@@ -154,7 +193,13 @@ def main(argv=None):
               f"{100*r['frac']:5.1f}% of {r['bound']}", file=sys.stderr, flush=True)
     dev.check_flags()
 
-    head = results.get("add")
+    head = results.get(HEADLINE)
+    roofline = None
+    if head:
+        roofline = {"bound": "mfma", "achieved": round(head["achieved"], 2),
+                    "peak": head["peak"], "unit": head["unit"],
+                    "frac": round(head["frac"], 4), "traffic": TRAFFIC.get(HEADLINE)}
+    base = None if args.no_cpu else cpu_baseline(orc)
     line = {
         "metric": METRIC,
         "value": round(head["achieved"], 2) if head else None,
@@ -168,7 +213,10 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: splitmix64/Box-Muller seeded inputs",
-        "config": {"workload": "C3 add, 33.5M-element f32 tensors"},
+        "config": {"workload": "C2 f32 matmul C[4096,4096] = A[4096,4096] B[4096,4096], "
+                               "row-major, entries U(-1,1)"},
+        "roofline": roofline,
+        "cpu_baseline": base,
         "device": {"name": info["name"], "arch": info["architecture"],
                    "compute_units": info["compute_units"]},
         "kernels": {k: {"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),

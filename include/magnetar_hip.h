@@ -175,6 +175,17 @@ void mhip_rope_params_default(mhip_rope_params* p, uint64_t dimension, uint64_t 
 mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t rows,
                           uint64_t cols, const mhip_rope_params* params);
 
+/* ---- matmul (src/kernels.rs:4388-4436, :5518-5789; src/kernels.cu:1262-1693) ---- */
+/* out[m, n] = A . B with A [m, k] (or [k, m] stored when transpose_a) and
+ * B [k, n] (or [n, k] when transpose_b), f32 accumulation; addend_mode 1 adds
+ * addend[col] (matmul-bias), 2 adds addend[row * n + col] (matmul-residual)
+ * to the finished sum. fp32 MFMA tiles for m > 8; an HBM-streaming split-k
+ * kernel for m <= 8 (decode), whose partial sums use a grow-only workspace
+ * owned by the context. */
+mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
+                            uint64_t m, uint64_t k, uint64_t n, int transpose_a,
+                            int transpose_b, const float* addend, int addend_mode);
+
 #ifdef __cplusplus
 }
 #endif

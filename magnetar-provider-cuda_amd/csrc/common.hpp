@@ -25,6 +25,9 @@ struct mhip_ctx {
         float* device = nullptr;
     };
     std::vector<RopeTable> rope_tables;
+    // Grow-only device workspace for split-k partial sums (matmul, attention).
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
 };
 
 namespace mhip {

@@ -109,6 +109,7 @@ mhip_status mhip_ctx_destroy(mhip_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->flags) (void)hipFree(ctx->flags);
     for (auto& table : ctx->rope_tables) (void)hipFree(table.device);
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
     if (ctx->timer_start) (void)hipEventDestroy(ctx->timer_start);
     if (ctx->timer_stop) (void)hipEventDestroy(ctx->timer_stop);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

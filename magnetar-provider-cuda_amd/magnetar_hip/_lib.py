@@ -134,6 +134,7 @@ SIGNATURES = {
     "mhip_softmax_rows_f32": [_CTX, _P, _P, _U64, _U64],
     "mhip_rope_params_default": [ctypes.POINTER(RopeParams), _U64, _U64],
     "mhip_rope_f32": [_CTX, _P, _P, _U64, _U64, ctypes.POINTER(RopeParams)],
+    "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
 }
 
 _RESTYPES = {

@@ -123,3 +123,16 @@ def rope(dev: Device, x: DeviceArray, params: _lib.RopeParams, out=None) -> Devi
     out = _out(dev, out, x.shape)
     call("mhip_rope_f32", dev.ctx, _p(x), _p(out), rows, cols, ctypes.byref(params))
     return out
+
+
+def matmul(dev: Device, a: DeviceArray, b: DeviceArray, transpose_a: bool = False,
+           transpose_b: bool = False, addend: DeviceArray | None = None, addend_mode: int = 0,
+           out=None) -> DeviceArray:
+    m, k = (a.shape[1], a.shape[0]) if transpose_a else (a.shape[0], a.shape[1])
+    k2, n = (b.shape[1], b.shape[0]) if transpose_b else (b.shape[0], b.shape[1])
+    if k != k2:
+        raise ValueError(f"matmul inner dimension mismatch: {k} vs {k2}")
+    out = _out(dev, out, (m, n))
+    call("mhip_matmul_f32", dev.ctx, _p(a), _p(b), _p(out), m, k, n, int(transpose_a),
+         int(transpose_b), _p(addend), addend_mode)
+    return out

@@ -1,0 +1,133 @@
+"""GPU parity: f32 matmul (MFMA tiles and the decode GEMV) against the CPU oracle.
+
+Bar (north star): within 1e-4 max relative error, measured normwise:
+max |gpu - cpu| / max |cpu| over the output (an output entry near zero after
+cancellation has no meaningful elementwise relative error; the normwise
+measure still catches a dropped or doubled k term, ~|a||b| / max|C| ~ 1e-3 at
+these sizes). Fused bias / residual epilogues must be bit-identical to the
+unfused matmul followed by add (src/tests_conformance.rs:293-408).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, max_normwise_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def run(dev, a, b, ta=False, tb=False, addend=None, mode=0):
+    from magnetar_hip import ops
+    return ops.matmul(dev, dev.upload(a), dev.upload(b), ta, tb,
+                      dev.upload(addend) if addend is not None else None, mode).numpy()
+
+
+def test_reference_fixtures(dev, orc):
+    """src/tests_conformance.rs:262-288 (plain and transposed a)."""
+    a = np.array([1, 2, 3, 4, 5, 6], np.float32).reshape(2, 3)
+    b = np.array([1, 0, 0, 1, 1, 1], np.float32).reshape(3, 2)
+    assert_bitexact(run(dev, a, b), orc.matmul(a, b)[0])
+    at = np.array([1, 4, 2, 5, 3, 6], np.float32).reshape(3, 2)
+    assert_bitexact(run(dev, at, b, ta=True), orc.matmul(at, b, True)[0])
+
+
+@pytest.mark.parametrize("m,k,n,ta", [(1, 1000, 70, False), (1, 37, 33, False),
+                                      (3, 129, 65, False), (5, 64, 1, False),
+                                      (4, 50, 40, True)])
+def test_reference_uneven_shapes(dev, orc, m, k, n, ta):
+    """src/tests_conformance.rs:447-481, with its `values` generator."""
+    a = orc.values(m * k, 1).reshape((k, m) if ta else (m, k))
+    b = orc.values(k * n, 2).reshape(k, n)
+    err = max_normwise_err(run(dev, a, b, ta), orc.matmul(a, b, ta)[0])
+    assert err <= TOL
+
+
+SHAPES = [(128, 128, 128), (256, 512, 384), (130, 33, 70), (129, 257, 131), (64, 4096, 64),
+          (9, 100, 300), (300, 7, 5), (512, 1024, 768), (1000, 1000, 1000), (32, 256, 688)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_mfma_shapes_and_transposes(dev, orc, m, k, n, ta, tb):
+    a = orc.uniform(m * k, 100 + m, -1.0, 1.0).reshape((k, m) if ta else (m, k))
+    b = orc.uniform(k * n, 200 + n, -1.0, 1.0).reshape((n, k) if tb else (k, n))
+    want, st = orc.matmul(a, b, ta, tb)
+    assert st == 0
+    err = max_normwise_err(run(dev, a, b, ta, tb), want)
+    print(f"matmul {m}x{k}x{n} ta={ta} tb={tb}: normwise err {err:.2e}")
+    assert err <= TOL
+
+
+def test_integer_inputs_are_exact(dev, orc):
+    """Small-integer operands: every partial sum is an exactly representable
+    integer, so any summation order gives the exact product."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(-8, 9, (200, 300)).astype(np.float32)
+    b = rng.integers(-8, 9, (300, 150)).astype(np.float32)
+    exact = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    assert_bitexact(run(dev, a, b), exact)
+    a1 = a[:3]
+    assert_bitexact(run(dev, a1, b[:, :148]), exact[:3, :148])
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 256), (130, 64, 96), (1, 300, 40), (8, 128, 64)])
+def test_fused_addend_is_bit_identical_to_unfused(dev, orc, m, k, n):
+    from magnetar_hip import ops
+    a = dev.upload(orc.values(m * k, 3).reshape(m, k))
+    b = dev.upload(orc.values(k * n, 4).reshape(k, n))
+    bias = dev.upload(orc.values(n, 5))
+    resid = dev.upload(orc.values(m * n, 6).reshape(m, n))
+    plain = ops.matmul(dev, a, b)
+    unfused_bias = ops.bias_add(dev, plain, bias).numpy()
+    unfused_res = ops.add(dev, plain, resid).numpy()
+    assert_bitexact(ops.matmul(dev, a, b, addend=bias, addend_mode=1).numpy(), unfused_bias)
+    assert_bitexact(ops.matmul(dev, a, b, addend=resid, addend_mode=2).numpy(), unfused_res)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+def test_decode_gemv_rows(dev, orc, m):
+    k, n = 4096, 1024
+    a = orc.uniform(m * k, 7, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 8, -1.0, 1.0).reshape(k, n)
+    err = max_normwise_err(run(dev, a, b), orc.matmul(a, b)[0])
+    assert err <= TOL
+
+
+def test_skinny_decode_baseline_shape(dev, orc):
+    """M=1, K=4096, N=11008."""
+    a = orc.uniform(4096, 11, -1.0, 1.0).reshape(1, 4096)
+    b = orc.uniform(4096 * 11008, 12, -1.0, 1.0).reshape(4096, 11008)
+    err = max_normwise_err(run(dev, a, b), orc.matmul(a, b)[0])
+    print(f"matmul 1x4096x11008: normwise err {err:.2e}")
+    assert err <= TOL
+
+
+def test_zero_inner_dimension(dev, orc):
+    a = np.zeros((3, 0), np.float32)
+    b = np.zeros((0, 4), np.float32)
+    from magnetar_hip import ops
+    bias = np.arange(4, dtype=np.float32)
+    got = ops.matmul(dev, dev.upload(a), dev.upload(b), addend=dev.upload(bias),
+                     addend_mode=1).numpy()
+    assert_bitexact(got, np.tile(bias, (3, 1)))
+
+
+@pytest.mark.parametrize("size", [2048, 4096])
+def test_square_baseline_sizes(dev, orc, size):
+    """Full-size products: 16 sampled rows against the oracle exactly as it
+    sums them, plus a checksum of the whole product, C x = A (B x), in f64."""
+    from magnetar_hip import ops
+    a = orc.uniform(size * size, 21, -1.0, 1.0).reshape(size, size)
+    b = orc.uniform(size * size, 22, -1.0, 1.0).reshape(size, size)
+    c = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
+    rows = np.linspace(0, size - 1, 16).astype(int)
+    for r in rows:
+        want = orc.matmul_rows(a, b, int(r), int(r) + 1)
+        assert max_normwise_err(c[r:r + 1], want) <= TOL
+    x = np.random.default_rng(0).standard_normal(size)
+    lhs = c.astype(np.float64) @ x
+    rhs = a.astype(np.float64) @ (b.astype(np.float64) @ x)
+    err = np.max(np.abs(lhs - rhs)) / np.max(np.abs(rhs))
+    print(f"matmul {size}^3 checksum err {err:.2e}")
+    assert err <= TOL
