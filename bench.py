@@ -127,6 +127,32 @@ def matmul_cases(dev, orc):
     return cases
 
 
+def attention_cases(dev, orc):
+    from magnetar_hip import ops
+    cases = []
+    B, S, H, d = 4, 2048, 32, 128
+    q = dev.upload(orc.normal(B * S * H * d, seed(4, 0)).reshape(B * S, H * d))
+    k = dev.upload(orc.normal(B * S * H * d, seed(4, 1)).reshape(B * S, H * d))
+    v = dev.upload(orc.normal(B * S * H * d, seed(4, 2)).reshape(B * S, H * d))
+    o = dev.empty((B * S, H * d))
+    p = ops.attention_params(S, S, H, d, causal=True, batch=B)
+    flops = 4.0 * d * S * (S + 1) / 2 * B * H
+    cases.append(Case("attention_prefill", lambda: ops.attention(dev, q, k, v, p, o), flops,
+                      "mfma", [B, H, S, d]))
+    B2, KV = 8, 4096
+    q2 = dev.upload(orc.normal(B2 * H * d, seed(4, 3)).reshape(B2, H * d))
+    k2 = dev.empty((B2 * KV, H * d))
+    v2 = dev.empty((B2 * KV, H * d))
+    _fill_normal(dev, k2, seed(4, 4))
+    _fill_normal(dev, v2, seed(4, 5))
+    o2 = dev.empty((B2, H * d))
+    p2 = ops.attention_params(1, KV, H, d, causal=True, batch=B2)
+    nbytes = 2 * B2 * KV * H * d * 4 + 2 * B2 * H * d * 4
+    cases.append(Case("attention_decode", lambda: ops.attention(dev, q2, k2, v2, p2, o2), nbytes,
+                      "hbm", [B2, H, KV, d]))
+    return cases
+
+
 def cpu_baseline(orc, budget_s=12.0):
     """The oracle's matmul (f32, k ascending, one thread) on whole rows of the
     4096^3 headline product, as many rows as fit the time budget."""
@@ -181,7 +207,7 @@ def main(argv=None):
 
     dev = magnetar_hip.Device(0)
     info = dev.info()
-    cases = matmul_cases(dev, orc) + streaming_cases(dev, orc)
+    cases = matmul_cases(dev, orc) + attention_cases(dev, orc) + streaming_cases(dev, orc)
     only = set(filter(None, args.only.split(",")))
     results = {}
     for case in cases:

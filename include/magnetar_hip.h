@@ -186,6 +186,35 @@ mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float
                             uint64_t m, uint64_t k, uint64_t n, int transpose_a,
                             int transpose_b, const float* addend, int addend_mode);
 
+/* ---- attention (src/kernels.rs:6505-7078; src/kernels.cu:1868-2787) ---- */
+typedef struct {
+    uint64_t seq_len;           /* query rows */
+    uint64_t kv_rows;           /* rows held by k and v */
+    uint64_t kv_seq_len;        /* key_count: keys in use, <= kv_rows (kv_rows when absent) */
+    uint64_t head_count;
+    uint64_t kv_head_count;     /* divides head_count (grouped-query attention) */
+    uint64_t head_dimension;
+    uint64_t value_dimension;   /* V and output width per head; 0 means head_dimension */
+    int causal;
+    int64_t window_size;        /* sliding window (causal only); -1 none, 0 rejected */
+    float scale;                /* factor on q.k; <= 0 means 1/sqrt(head_dimension) */
+    /* Batched extension: `batch` independent calls with these element strides
+     * (0: densely packed); the reference has no batch dimension. */
+    uint64_t batch;
+    uint64_t q_batch_stride;
+    uint64_t kv_batch_stride;
+    uint64_t v_batch_stride;
+    uint64_t out_batch_stride;
+} mhip_attention_params;
+/* q [seq, H*d], k [kv_rows, Hkv*d], v [kv_rows, Hkv*vd] -> out [seq, H*vd].
+ * Query i sits at position (kv_seq_len - seq_len) + i; a causal query admits
+ * keys up to its own position, a window of w the last w of them. Softmax of
+ * q.k * scale over the admitted keys weights V rows; no admitted key gives 0.
+ * fp32 MFMA flash prefill for head dims 64/128, split-KV decode for one query
+ * row (workspace owned by the context), a generic kernel otherwise. */
+mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
+                               float* out, const mhip_attention_params* params);
+
 #ifdef __cplusplus
 }
 #endif

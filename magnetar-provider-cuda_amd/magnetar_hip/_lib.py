@@ -89,6 +89,7 @@ class AttentionParams(ctypes.Structure):
         ("batch", ctypes.c_uint64),
         ("q_batch_stride", ctypes.c_uint64),
         ("kv_batch_stride", ctypes.c_uint64),
+        ("v_batch_stride", ctypes.c_uint64),
         ("out_batch_stride", ctypes.c_uint64),
     ]
 
@@ -135,6 +136,7 @@ SIGNATURES = {
     "mhip_rope_params_default": [ctypes.POINTER(RopeParams), _U64, _U64],
     "mhip_rope_f32": [_CTX, _P, _P, _U64, _U64, ctypes.POINTER(RopeParams)],
     "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
+    "mhip_attention_f32": [_CTX, _P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
 }
 
 _RESTYPES = {

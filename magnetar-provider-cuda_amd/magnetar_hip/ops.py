@@ -136,3 +136,29 @@ def matmul(dev: Device, a: DeviceArray, b: DeviceArray, transpose_a: bool = Fals
     call("mhip_matmul_f32", dev.ctx, _p(a), _p(b), _p(out), m, k, n, int(transpose_a),
          int(transpose_b), _p(addend), addend_mode)
     return out
+
+
+def attention_params(seq_len, kv_rows, head_count, head_dimension, kv_head_count=None,
+                     value_dimension=None, causal=False, window_size=None, key_count=None,
+                     scale=None, batch=1) -> _lib.AttentionParams:
+    p = _lib.AttentionParams()
+    p.seq_len, p.kv_rows = seq_len, kv_rows
+    p.kv_seq_len = key_count if key_count is not None else kv_rows
+    p.head_count = head_count
+    p.kv_head_count = kv_head_count if kv_head_count is not None else head_count
+    p.head_dimension = head_dimension
+    p.value_dimension = value_dimension if value_dimension is not None else head_dimension
+    p.causal = int(bool(causal))
+    p.window_size = -1 if window_size is None else window_size
+    p.scale = 0.0 if scale is None else scale
+    p.batch = batch
+    return p
+
+
+def attention(dev: Device, q: DeviceArray, k: DeviceArray, v: DeviceArray,
+              params: _lib.AttentionParams, out=None) -> DeviceArray:
+    batch = max(1, params.batch)
+    rows = params.seq_len * batch
+    out = _out(dev, out, (rows, params.head_count * params.value_dimension))
+    call("mhip_attention_f32", dev.ctx, _p(q), _p(k), _p(v), _p(out), ctypes.byref(params))
+    return out
