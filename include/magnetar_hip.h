@@ -215,6 +215,192 @@ typedef struct {
 mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
                                float* out, const mhip_attention_params* params);
 
+/* ======================================================================== */
+/* Executor: the `CudaExecutor`-shaped ProviderExecutionApi (src/executor.rs) */
+/* ======================================================================== */
+/* Tensors are device-resident buffers keyed by resource id (src/executor.rs:101);
+ * invocations name a Kernel and its inputs/outputs by id, with typed
+ * attributes, and run eagerly on submit (src/executor.rs:2191-2241). No device
+ * pointer ever crosses this part of the interface. */
+
+typedef struct mhip_executor mhip_executor;
+
+typedef enum { MHIP_DTYPE_F32 = 0, MHIP_DTYPE_F16 = 1, MHIP_DTYPE_BF16 = 2 } mhip_dtype;
+
+/* `KernelError` categories (src/error.rs:97-133 plus the executor's own). */
+typedef enum {
+    MHIP_KERNEL_OK = 0,
+    MHIP_KERNEL_SHAPE_UNSUPPORTED = 1,
+    MHIP_KERNEL_DTYPE_UNSUPPORTED = 2,
+    MHIP_KERNEL_LAYOUT_UNSUPPORTED = 3,
+    MHIP_KERNEL_DEVICE_UNSUPPORTED = 4,
+    MHIP_KERNEL_OUT_OF_DEVICE_MEMORY = 5,
+    MHIP_KERNEL_EXECUTION_FAILED = 6,
+    MHIP_KERNEL_ATTRIBUTE_UNSUPPORTED = 7,
+    MHIP_KERNEL_NOT_FOUND = 8,
+    MHIP_KERNEL_TIMEOUT = 9
+} mhip_kernel_error;
+
+/* `OperatorAttributeValue` (src/executor.rs:1141-1185). */
+typedef enum {
+    MHIP_ATTR_FLOAT = 0,
+    MHIP_ATTR_INTEGER = 1,
+    MHIP_ATTR_BOOLEAN = 2,
+    MHIP_ATTR_STRING = 3,
+    MHIP_ATTR_DTYPE = 4
+} mhip_attr_kind;
+
+typedef struct {
+    const char* key;
+    int kind;               /* mhip_attr_kind */
+    double f;
+    int64_t i;
+    int b;
+    const char* s;
+    int dtype;              /* mhip_dtype */
+} mhip_attribute;
+
+typedef struct {
+    const char* id;
+    int dtype;              /* mhip_dtype of the descriptor */
+    const uint64_t* shape;
+    int rank;
+} mhip_tensor_ref;
+
+typedef struct {
+    const char* invocation_id;
+    const char* kernel_name;
+    const mhip_tensor_ref* inputs;
+    int input_count;
+    const mhip_tensor_ref* outputs;
+    int output_count;
+    const mhip_attribute* attributes;
+    int attribute_count;
+    int64_t deadline_millis;   /* -1: none; 0 fails with MHIP_KERNEL_TIMEOUT */
+} mhip_invocation;
+
+/* `KernelObservation` kinds (src/executor.rs:1082-1100, :1197-1231). */
+typedef enum {
+    MHIP_OBS_DISPATCH_STARTED = 0,
+    MHIP_OBS_DISPATCH_COMPLETED = 1,
+    MHIP_OBS_DISPATCH_FAILED = 2,
+    MHIP_OBS_TIMEOUT = 3
+} mhip_observation_kind;
+
+typedef struct {
+    int kind;               /* mhip_observation_kind */
+    char kernel[64];
+    char invocation[64];
+    int error;              /* mhip_kernel_error for DISPATCH_FAILED */
+} mhip_observation;
+
+mhip_status mhip_executor_create(mhip_ctx* ctx, const char* device_id, const char* provider_name,
+                                 mhip_executor** out);
+mhip_status mhip_executor_destroy(mhip_executor* ex);
+/* The detail text of the calling thread's last executor failure. */
+const char* mhip_executor_last_detail(void);
+
+/* write_tensor / write_weight_tensor (src/executor.rs:394-418): `data` holds
+ * f32 values for MHIP_DTYPE_F32, 2-byte bit patterns for F16/BF16. */
+mhip_kernel_error mhip_executor_write_tensor(mhip_executor* ex, const char* id,
+                                             const uint64_t* shape, int rank, int dtype,
+                                             const void* data, size_t bytes);
+/* f32 host values stored as `dtype`, encoded RNE on the device (upload_half,
+ * src/kernels.rs:2172-2197). */
+mhip_kernel_error mhip_executor_write_tensor_values(mhip_executor* ex, const char* id,
+                                                    const uint64_t* shape, int rank, int dtype,
+                                                    const float* values);
+mhip_kernel_error mhip_executor_write_zeroed_tensor(mhip_executor* ex, const char* id,
+                                                    const uint64_t* shape, int rank, int dtype);
+/* read_tensor (src/executor.rs:430-434): the stored bytes, waiting for the device. */
+mhip_kernel_error mhip_executor_read_tensor(mhip_executor* ex, const char* id, void* dst,
+                                            size_t capacity, size_t* written);
+/* The stored values decoded to f32 (download_half, src/kernels.rs:2203-2219). */
+mhip_kernel_error mhip_executor_read_tensor_values(mhip_executor* ex, const char* id, float* dst,
+                                                   size_t capacity);
+/* read_tensor_rows (src/executor.rs:2392-2414): rows of a rank >= 1 f32 tensor. */
+mhip_kernel_error mhip_executor_read_tensor_rows(mhip_executor* ex, const char* id,
+                                                 uint64_t row_begin, uint64_t row_count,
+                                                 float* dst, size_t capacity);
+/* resident_shape: rank and dtype too; shape holds up to 8 dims. */
+mhip_kernel_error mhip_executor_resident_shape(mhip_executor* ex, const char* id, uint64_t* shape,
+                                               int* rank, int* dtype);
+mhip_kernel_error mhip_executor_release_tensor(mhip_executor* ex, const char* id);
+mhip_kernel_error mhip_executor_copy_tensor(mhip_executor* ex, const char* src, const char* dst);
+uint64_t mhip_executor_tensor_count(mhip_executor* ex);
+
+/* submit_kernel / complete_kernel (src/executor.rs:2322-2330, :2222-2241):
+ * submit runs the invocation eagerly and parks its result under `handle`;
+ * complete returns that result (MHIP_KERNEL_OK or the failure) exactly once. */
+mhip_kernel_error mhip_executor_submit_kernel(mhip_executor* ex, const mhip_invocation* inv,
+                                              uint64_t* handle);
+mhip_kernel_error mhip_executor_complete_kernel(mhip_executor* ex, uint64_t handle);
+/* submit + complete in one call. */
+mhip_kernel_error mhip_executor_execute(mhip_executor* ex, const mhip_invocation* inv);
+/* MAGNETAR_HIP_SYNC_NODES equivalent: wait for the device after each dispatch. */
+mhip_status mhip_executor_set_sync_nodes(mhip_executor* ex, int enabled);
+/* The observation log (last 4096 entries, src/executor.rs:82). */
+uint64_t mhip_executor_observation_count(mhip_executor* ex);
+mhip_status mhip_executor_observation(mhip_executor* ex, uint64_t index, mhip_observation* out);
+
+/* ======================================================================== */
+/* Provider facade and Kernel advertisements (src/provider.rs, advertisements.rs) */
+/* ======================================================================== */
+
+typedef enum {
+    MHIP_HEALTH_AVAILABLE = 0,
+    MHIP_HEALTH_DEGRADED = 1,
+    MHIP_HEALTH_UNAVAILABLE = 2
+} mhip_health;
+
+typedef struct mhip_provider mhip_provider;
+
+typedef struct {
+    char name[128];
+    char version[32];
+    char vendor[64];
+    char description[160];
+} mhip_provider_metadata;
+
+typedef struct {
+    char id[32];                /* "hip:<ordinal>" */
+    char name[256];
+    char architecture[64];
+    uint64_t memory_capacity;
+    uint32_t compute_units;
+    int pressure;               /* as mhip_device_info.pressure */
+} mhip_device_descriptor;
+
+/* Never fails for lack of hardware: with no device the provider reports
+ * MHIP_HEALTH_UNAVAILABLE, zero devices and zero advertisements. */
+mhip_status mhip_provider_create(int ordinal, const char* provider_name, mhip_provider** out);
+mhip_status mhip_provider_destroy(mhip_provider* p);
+mhip_status mhip_provider_metadata_get(mhip_provider* p, mhip_provider_metadata* out);
+int mhip_provider_health(mhip_provider* p);
+int mhip_provider_device_count(mhip_provider* p);
+mhip_status mhip_provider_device(mhip_provider* p, int index, mhip_device_descriptor* out);
+/* The provider's executor (NULL unless healthy); owned by the provider. */
+mhip_executor* mhip_provider_executor(mhip_provider* p);
+mhip_status mhip_provider_initialize(mhip_provider* p);
+mhip_status mhip_provider_shutdown(mhip_provider* p);
+
+typedef struct {
+    char name[48];              /* Kernel name, e.g. "matmul", "add-half" */
+    char operator_name[48];     /* portable Operator, e.g. "add" for "add-half" */
+    char operator_family[32];   /* LinearAlgebra, Tensor, Activation, ... */
+    uint32_t input_dtypes;      /* bit (1 << mhip_dtype) per accepted dtype */
+    uint32_t output_dtypes;
+    int rank;                   /* required rank, 0 when any */
+    char features[256];         /* comma-separated optional forms honoured */
+    char conformance_profile[32];
+    char family[16];            /* implementation family: "Hip" */
+    char device_id[32];
+    char provider[128];
+} mhip_advertisement;
+
+int mhip_provider_advertisement_count(mhip_provider* p);
+mhip_status mhip_provider_advertisement(mhip_provider* p, int index, mhip_advertisement* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,280 @@
+"""GPU: the Provider facade and the executor's dispatch contract.
+
+Mirrors the reference's integration tier (src/tests.rs:80-165,
+src/tests_hardware_hot_path.rs:134-595): Kernels dispatched by name through
+submit_kernel / complete_kernel with Runtime-style attributes; results stay
+device-resident between calls; failures keep the overwritten output's value;
+errors surface in the reference's categories.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, max_normwise_err, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def provider():
+    import magnetar_hip
+    p = magnetar_hip.Provider()
+    yield p
+    p.close()
+
+
+@pytest.fixture()
+def ex(provider):
+    ex = provider.execution_api()
+    assert ex is not None
+    return ex
+
+
+def inv(kernel, inputs, output, attrs=None, **kw):
+    from magnetar_hip import KernelInvocation, TensorRef
+    ins = [i if isinstance(i, TensorRef) else TensorRef(i) for i in inputs]
+    out = output if isinstance(output, TensorRef) else TensorRef(output)
+    return KernelInvocation(kernel, ins, [out], attrs or {}, **kw)
+
+
+def test_provider_reports_the_device(provider):
+    assert provider.health() == "Available"
+    devices = provider.devices()
+    assert len(devices) == 1
+    assert devices[0]["id"] == "hip:0"
+    assert devices[0]["memory_capacity"] > 0
+    assert "gfx950" in devices[0]["architecture"]
+    assert devices[0]["compute_units"] > 0
+
+
+def test_advertisements(provider):
+    adverts = provider.kernel_advertisements()
+    names = [a.name for a in adverts]
+    assert names == ["matmul", "matmul-bias", "matmul-residual", "silu-mul", "gated-matmul",
+                     "embedding", "rmsnorm", "rope", "attention", "softmax", "silu", "add", "mul",
+                     "concat", "residual-add", "add-half", "mul-half"]
+    by = {a.name: a for a in adverts}
+    for name in ("matmul", "rope", "attention", "softmax"):
+        assert by[name].rank == 2
+    assert by["add-half"].operator_name == "add" and by["mul-half"].operator_name == "mul"
+    assert by["add-half"].input_dtypes == [1, 2]
+    assert by["add"].input_dtypes == [0]
+    assert "rmsnorm-without-weight" in by["rmsnorm"].features
+    assert all(a.conformance_profile == "hip-conformance-v1" for a in adverts)
+    assert all(a.device_id == "hip:0" for a in adverts)
+
+
+def test_every_kernel_through_dispatch(ex, orc):
+    """One invocation per advertised f32 Kernel, checked against the oracle."""
+    rows, hidden, heads, hd, ffn = 8, 64, 4, 16, 96
+    x = orc.hashed_values(rows * hidden, 1).reshape(rows, hidden)
+    y = orc.hashed_values(rows * hidden, 2).reshape(rows, hidden)
+    w = orc.hashed_values(hidden * ffn, 3).reshape(hidden, ffn)
+    g = orc.normal(hidden, 4, 1.0, 0.1)
+    table = orc.normal(50 * hidden, 5).reshape(50, hidden)
+    ids = np.array([3, 0, 49, 7], np.float32)
+    for name, arr in dict(x=x, y=y, w=w, g=g, table=table, ids=ids).items():
+        ex.write_tensor(name, arr)
+    ex.execute(inv("add", ["x", "y"], "o"))
+    assert_bitexact(ex.read_tensor("o"), orc.add(x, y)[0])
+    ex.execute(inv("residual-add", ["x", "y"], "o"))
+    assert_bitexact(ex.read_tensor("o"), orc.add(x, y)[0])
+    ex.execute(inv("add", ["x", "g"], "o"))  # bias broadcast
+    assert_bitexact(ex.read_tensor("o"), orc.bias_add(x, g)[0])
+    ex.execute(inv("mul", ["x", "y"], "o"))
+    assert_bitexact(ex.read_tensor("o"), orc.mul(x, y)[0])
+    ex.write_tensor("s", np.array([0.25], np.float32))
+    ex.execute(inv("mul", ["x", "s"], "o"))  # [1] scalar broadcast
+    assert_bitexact(ex.read_tensor("o"), x * np.float32(0.25))
+    ex.execute(inv("silu", ["x"], "o"))
+    assert max_rel_err(ex.read_tensor("o"), orc.silu(x)[0], 1e-37) <= 1e-6
+    ex.execute(inv("silu-mul", ["x", "y"], "o"))
+    assert max_rel_err(ex.read_tensor("o"), orc.silu_mul(x, y)[0], 1e-37) <= 1e-6
+    ex.execute(inv("softmax", ["x"], "o"))
+    assert max_rel_err(ex.read_tensor("o"), orc.softmax_rows(x)[0]) <= 1e-4
+    ex.execute(inv("rmsnorm", ["x", "g"], "o", {"epsilon": 1e-5}))
+    assert max_rel_err(ex.read_tensor("o"), orc.rmsnorm(x, g, 1e-5)[0]) <= 1e-4
+    ex.execute(inv("rmsnorm", ["x"], "o"))  # no weight, default epsilon 1e-6
+    assert max_rel_err(ex.read_tensor("o"), orc.rmsnorm(x, None, 1e-6)[0]) <= 1e-4
+    ex.execute(inv("rmsnorm", ["x"], "o",
+                   {"head_count": heads, "head_dimension": hd}))
+    assert max_rel_err(ex.read_tensor("o"), orc.rmsnorm(x, None, 1e-6, cols=hd)[0]) <= 1e-4
+    ex.execute(inv("embedding", ["table", "ids"], "o"))
+    assert_bitexact(ex.read_tensor("o"), table[[3, 0, 49, 7]])
+    ex.execute(inv("embedding", ["table", "ids"], "o", {"scale": 8.0}))
+    assert_bitexact(ex.read_tensor("o"), table[[3, 0, 49, 7]] * np.float32(8.0))
+    ex.execute(inv("matmul", ["x", "w"], "o"))
+    assert max_normwise_err(ex.read_tensor("o"), orc.matmul(x, w)[0]) <= 1e-4
+    ex.write_tensor("bias", orc.hashed_values(ffn, 6))
+    ex.execute(inv("matmul-bias", ["x", "w", "bias"], "o"))
+    plain = orc.matmul(x, w)[0]
+    assert max_normwise_err(ex.read_tensor("o"), plain + orc.hashed_values(ffn, 6)) <= 1e-4
+    ex.write_tensor("w2", orc.hashed_values(hidden * ffn, 7).reshape(hidden, ffn))
+    ex.execute(inv("gated-matmul", ["x", "w", "w2"], "o"))
+    gate = orc.matmul(x, w)[0]
+    up = orc.matmul(x, orc.hashed_values(hidden * ffn, 7).reshape(hidden, ffn))[0]
+    assert max_normwise_err(ex.read_tensor("o"), orc.silu_mul(gate, up)[0]) <= 1e-4
+    ex.execute(inv("rope", ["x"], "o", {"dimension": hd, "head_count": heads,
+                                        "position_offset": 5}))
+    want, _ = orc.rope(x, orc.rope_params(hd, heads, position_offset=5))
+    assert np.max(np.abs(ex.read_tensor("o") - want)) <= 1e-6
+    ex.execute(inv("attention", ["x", "y", "x"], "o", {"head_count": heads, "head_dimension": hd,
+                                                       "causal": True}))
+    want, _ = orc.attention(x, y, x, orc.attention_params(rows, rows, heads, hd, causal=True))
+    assert max_normwise_err(ex.read_tensor("o"), want) <= 1e-4
+    ex.execute(inv("concat", ["x", "y"], "o"))
+    assert_bitexact(ex.read_tensor("o"), np.concatenate([x, y]))
+
+
+def test_device_resident_chain(ex, orc):
+    """weight -> matmul -> rmsnorm -> rope -> projection, never leaving the
+    device (src/tests_hardware_hot_path.rs:339-526), against the CPU chain."""
+    seq, hidden, heads = 32, 256, 4
+    x = orc.normal(seq * hidden, 11, 0.0, 1.0).reshape(seq, hidden)
+    wq = orc.normal(hidden * hidden, 12, 0.0, 0.02).reshape(hidden, hidden)
+    wo = orc.normal(hidden * hidden, 13, 0.0, 0.02).reshape(hidden, hidden)
+    gain = np.ones(hidden, np.float32)
+    for name, arr in dict(x=x, wq=wq, wo=wo, gain=gain).items():
+        ex.write_tensor(name, arr)
+    ex.execute(inv("matmul", ["x", "wq"], "q"))
+    ex.execute(inv("rmsnorm", ["q", "gain"], "qn", {"epsilon": 1e-5}))
+    ex.execute(inv("rope", ["qn"], "qr", {"dimension": 64, "head_count": heads}))
+    ex.execute(inv("matmul", ["qr", "wo"], "out"))
+    q, _ = orc.matmul(x, wq)
+    qn, _ = orc.rmsnorm(q, gain, 1e-5)
+    qr, _ = orc.rope(qn, orc.rope_params(64, heads))
+    want, _ = orc.matmul(qr, wo)
+    assert max_normwise_err(ex.read_tensor("out"), want) <= 1e-4
+    assert ex.resident_shape("out") == ((seq, hidden), 0)
+    rows = ex.read_tensor_rows("out", 5, 3)
+    assert_bitexact(rows, ex.read_tensor("out")[5:8])
+
+
+def test_attribute_errors(ex):
+    from magnetar_hip import KernelError, Integer, String, DType, F16
+    ex.write_tensor("a", np.ones((4, 8), np.float32))
+    ex.write_tensor("b", np.ones((8, 4), np.float32))
+    cases = [
+        (inv("rope", ["a"], "o", {}), "KernelAttributeUnsupported"),  # dimension required
+        (inv("rope", ["a"], "o", {"dimension": 4, "position_offset": Integer(-1)}), "KernelAttributeUnsupported"),
+        (inv("rope", ["a"], "o", {"dimension": 4, "position_offset": "3"}), "KernelAttributeUnsupported"),
+        (inv("rope", ["a"], "o", {"dimension": 4, "rotation_pairing": "neox"}), "KernelAttributeUnsupported"),
+        (inv("rope", ["a"], "o", {"dimension": 4, "position_mode": "explicit"}), "KernelAttributeUnsupported"),
+        (inv("rope", ["a"], "o", {"dimension": 4, "partial_rotary_factor": 1.5}), "KernelAttributeUnsupported"),
+        (inv("rope", ["a"], "o", {"dimension": 5}), "KernelShapeUnsupported"),
+        (inv("attention", ["a", "a", "a"], "o", {"head_dimension": 8}), "KernelAttributeUnsupported"),
+        (inv("attention", ["a", "a", "a"], "o", {"head_count": 1, "head_dimension": 8,
+                                                "attention_mask_kind": "causal"}), "KernelAttributeUnsupported"),
+        (inv("attention", ["a", "a", "a"], "o", {"head_count": 1, "head_dimension": 8,
+                                                "window_size": 4}), "KernelShapeUnsupported"),
+        (inv("attention", ["a", "a", "a"], "o", {"head_count": 1, "head_dimension": 8,
+                                                "scale": Integer(2)}), "KernelAttributeUnsupported"),
+        (inv("rmsnorm", ["a", "a"], "o", {"with_scale": False}), "KernelAttributeUnsupported"),
+        (inv("rmsnorm", ["a"], "o", {"head_count": 2}), "KernelAttributeUnsupported"),
+        (inv("rmsnorm", ["a"], "o", {"epsilon": -1.0}), "KernelShapeUnsupported"),
+        (inv("matmul", ["a", "b"], "o", {"accumulation_dtype": DType(F16)}), "KernelDTypeUnsupported"),
+        (inv("matmul", ["a", "a"], "o"), "KernelShapeUnsupported"),
+        (inv("mul", ["a", "b"], "o"), "KernelShapeUnsupported"),
+        (inv("add", ["a", "b"], "o"), "KernelShapeUnsupported"),
+        (inv("no-such-kernel", ["a"], "o"), "KernelNotFound"),
+        (inv("add", ["a", "missing"], "o"), "KernelExecutionFailed"),
+        (inv("embedding", ["a", "a"], "o", {"scale": Integer(3)}), "KernelAttributeUnsupported"),
+    ]
+    for invocation, code in cases:
+        with pytest.raises(KernelError) as err:
+            ex.execute(invocation)
+        assert err.value.code == code, (invocation.kernel, invocation.attributes, err.value)
+
+
+def test_deadline_zero_times_out(ex):
+    from magnetar_hip import KernelError
+    ex.write_tensor("a", np.ones(4, np.float32))
+    with pytest.raises(KernelError) as err:
+        ex.execute(inv("silu", ["a"], "o", deadline_millis=0))
+    assert err.value.code == "KernelTimeout"
+    kinds = [o[0] for o in ex.observations()[-2:]]
+    assert kinds == ["KernelDispatchStarted", "KernelTimeout"]
+
+
+def test_failed_dispatch_keeps_the_output_value(ex):
+    """src/tests_hardware_hot_path.rs:261-330: a failing invocation whose
+    output resource already holds a value leaves that value in place."""
+    from magnetar_hip import KernelError
+    ex.write_tensor("a", np.arange(6, dtype=np.float32).reshape(2, 3))
+    ex.write_tensor("bad", np.arange(4, dtype=np.float32).reshape(2, 2))
+    ex.write_tensor("keep", np.full((2, 3), 7.0, np.float32))
+    with pytest.raises(KernelError):
+        ex.execute(inv("add", ["a", "bad"], "keep"))
+    assert_bitexact(ex.read_tensor("keep"), np.full((2, 3), 7.0, np.float32))
+    # An invalid embedding id fails through the device flag, also keeping the value.
+    ex.write_tensor("table", np.zeros((4, 3), np.float32))
+    ex.write_tensor("ids", np.array([9.0], np.float32))
+    with pytest.raises(KernelError) as err:
+        ex.execute(inv("embedding", ["table", "ids"], "keep"))
+    assert err.value.code == "KernelShapeUnsupported"
+    assert "valid in-range" in err.value.detail
+    assert_bitexact(ex.read_tensor("keep"), np.full((2, 3), 7.0, np.float32))
+    # The same resource overwritten successfully reuses or replaces it.
+    ex.execute(inv("add", ["a", "a"], "keep"))
+    assert_bitexact(ex.read_tensor("keep"), np.arange(6, dtype=np.float32).reshape(2, 3) * 2)
+
+
+def test_output_reading_its_own_input(ex):
+    ex.write_tensor("acc", np.ones((3, 4), np.float32))
+    ex.write_tensor("one", np.ones((3, 4), np.float32))
+    for _ in range(3):
+        ex.execute(inv("add", ["acc", "one"], "acc"))
+    assert_bitexact(ex.read_tensor("acc"), np.full((3, 4), 4.0, np.float32))
+
+
+def test_softmax_without_finite_entry_fails(ex):
+    from magnetar_hip import KernelError
+    ex.write_tensor("m", np.full((2, 3), -np.inf, np.float32))
+    with pytest.raises(KernelError) as err:
+        ex.execute(inv("softmax", ["m"], "o"))
+    assert err.value.code == "KernelExecutionFailed"
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_half_kernels_through_dispatch(ex, orc, dtype):
+    """add-half / mul-half on 2-byte resident tensors, bit-exact against the
+    reference's model (src/tests_hardware_hot_path.rs:539-626)."""
+    from magnetar_hip import TensorRef
+    a = orc.normal(1000, 21)
+    b = orc.normal(1000, 22)
+    ha, hb = orc.encode_half(a, dtype - 1), orc.encode_half(b, dtype - 1)
+    ex.write_tensor("ha", ha, dtype)
+    ex.write_tensor_values("hb", b, dtype)  # encoded on the device
+    assert_bitexact(ex.read_tensor("hb"), hb)
+    for kernel, op in (("add-half", "add"), ("mul-half", "mul")):
+        ex.execute(inv(kernel, [TensorRef("ha", (1000,), dtype), TensorRef("hb", (1000,), dtype)],
+                       TensorRef("ho", (1000,), dtype)))
+        got = ex.read_tensor("ho")
+        assert got.dtype == np.uint16
+        assert_bitexact(got, orc.half_binary(ha, hb, dtype - 1, op))
+        assert_bitexact(ex.read_tensor_values("ho"), orc.decode_half(got, dtype - 1))
+    # f32-stored operands are encoded on the device, as the reference encodes on upload.
+    ex.write_tensor("fa", a)
+    ex.execute(inv("add-half", [TensorRef("fa", (1000,), dtype), TensorRef("hb", (1000,), dtype)],
+                   TensorRef("ho", (1000,), dtype)))
+    assert_bitexact(ex.read_tensor("ho"), orc.half_binary(ha, hb, dtype - 1, "add"))
+
+
+def test_half_kernel_rejects_f32_dtype(ex):
+    from magnetar_hip import KernelError, TensorRef
+    ex.write_tensor("fa", np.ones(4, np.float32))
+    with pytest.raises(KernelError) as err:
+        ex.execute(inv("add-half", [TensorRef("fa"), TensorRef("fa")], TensorRef("o")))
+    assert err.value.code == "KernelDTypeUnsupported"
+
+
+def test_observations_and_release(ex):
+    ex.write_tensor("r", np.ones(8, np.float32))
+    ex.execute(inv("silu", ["r"], "r2", id="obs-1"))
+    obs = ex.observations()
+    assert obs[-2][:3] == ("KernelDispatchStarted", "silu", "obs-1")
+    assert obs[-1][:3] == ("KernelDispatchCompleted", "silu", "obs-1")
+    n = ex.tensor_count()
+    ex.release_tensor("r2")
+    assert ex.tensor_count() == n - 1
+    ex.copy_tensor("r", "r3")
+    assert_bitexact(ex.read_tensor("r3"), np.ones(8, np.float32))
