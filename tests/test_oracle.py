@@ -1,0 +1,451 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+The reference's true oracle (magnetar_provider_cpu::*, crate magnetar-provider-cpu
+1.0.0, a path dependency with no pinned revision, Cargo.lock:909-916) is not in
+this container and its host language (Rust) cannot be built here. Each
+function of the restatement is instead checked against something a plausible
+mistake (a dropped term, a wrong sign, index or operand order) would fail:
+
+  function          pinned by
+  ---------------   ----------------------------------------------------------
+  half codec        the reference's exhaustive 65,536-pattern round trips
+                    (half_precision.rs:127-163); numpy float16 conversions over
+                    every sign/exponent with rounding-critical mantissas; an
+                    independent bfloat16 RNE; the reference's fixtures (golden)
+  half add/mul      numpy f32 arithmetic on decoded operands, re-encoded
+  add/mul/bias/     numpy float32 arithmetic (one IEEE op: exact); fixtures
+   scale/mul-scalar
+  silu, silu-mul    float64 closed form within 2 ulp; special values
+  embedding         the reference's fixture and invalid-id cases; exact copies
+  rmsnorm           float64 closed form; constant-row closed form; per-row weights
+  softmax           float64 closed form; rows sum to 1; shift invariance;
+                    masked (-inf) entries; the all -inf failure
+  rope              float64 textbook rotation on the reference's fixtures;
+                    position 0 is the identity; pair norms preserved; half-split
+                    equals interleaved under the pair permutation; banded/YaRN
+                    frequency bands
+  matmul            exact integer products; float64 brute force within the
+                    gamma_k summation bound; transposes; fused addends
+  attention         float64 textbook softmax(q k^T s + mask) v incl. GQA and
+                    windows; single key -> v; the 1e38 known answer
+
+Not pinnable here: the exact ulp choices of the reference CPU's expf / sinf /
+cosf / powf (Rust libm) -- bounded by the closed-form checks above.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, max_normwise_err, max_rel_err
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "reference_fixtures.json")
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return json.load(open(GOLDEN))
+
+
+# ---- generators -----------------------------------------------------------
+
+def test_generators_match_the_reference_formulas(orc):
+    i = np.arange(10, dtype=np.uint64)
+    want = (((i * 7919 + 3 * 104729) % 2001).astype(np.float32) - np.float32(1000.0)) * np.float32(1e-4)
+    assert_bitexact(orc.values(10, 3), want)
+    want = ((i * 7919 + 5 * 104729) % 2003).astype(np.float32) / np.float32(2003.0) - np.float32(0.5)
+    assert_bitexact(orc.attention_values(10, 5), want)
+    # splitmix64, src/tests_conformance.rs:2116-2128, in Python integers.
+    mask = (1 << 64) - 1
+    state = (0x9E3779B97F4A7C15 ^ (7 * 0xBF58476D1CE4E5B9)) & mask
+    vals = []
+    for _ in range(5):
+        state = (state + 0x9E3779B97F4A7C15) & mask
+        z = state
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        z ^= z >> 31
+        vals.append(np.float32(z >> 40) / np.float32(1 << 24) - np.float32(0.5))
+    assert_bitexact(orc.hashed_values(5, 7), np.array(vals, np.float32))
+    x = orc.normal(100000, 1)
+    assert abs(float(x.mean())) < 0.02 and abs(float(x.std()) - 1.0) < 0.02
+    u = orc.uniform(100000, 2, -1.0, 1.0)
+    assert u.min() >= -1.0 and u.max() < 1.0
+    ids = orc.token_ids(1000, 3, 50)
+    assert np.all(ids == np.floor(ids)) and ids.min() >= 0 and ids.max() < 50
+
+
+# ---- half codec --------------------------------------------------------------
+
+ALL16 = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+
+
+def f16_nan(h):
+    h = h.astype(np.uint32)
+    return ((h & 0x7C00) == 0x7C00) & ((h & 0x3FF) != 0)
+
+
+def bf16_nan(h):
+    h = h.astype(np.uint32)
+    return ((h & 0x7F80) == 0x7F80) & ((h & 0x7F) != 0)
+
+
+def rounding_critical_f32():
+    """Every sign and exponent with mantissas around each rounding boundary."""
+    sign_exp = np.arange(512, dtype=np.uint32) << 23
+    hi = np.arange(1 << 10, dtype=np.uint32) << 13
+    lows = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    mant = (hi[:, None] | lows[None, :]).reshape(-1) & 0x7FFFFF
+    return (sign_exp[:, None] | mant[None, :]).reshape(-1).view(np.float32)
+
+
+def test_half_round_trips_every_pattern(orc):
+    """src/half_precision.rs:136-162."""
+    for dt, isnan in ((0, f16_nan), (1, bf16_nan)):
+        dec = orc.decode_half(ALL16, dt)
+        enc = orc.encode_half(dec, dt)
+        nan = isnan(ALL16)
+        assert_bitexact(enc[~nan], ALL16[~nan])
+        assert np.all(isnan(enc[nan]))
+
+
+def test_f16_codec_against_numpy(orc):
+    dec = orc.decode_half(ALL16, 0)
+    ref = ALL16.view(np.float16).astype(np.float32)
+    nan = f16_nan(ALL16)
+    assert_bitexact(dec[~nan], ref[~nan])
+    # NaN payload kept, not quieted: sign | 0x7F800000 | mant << 13.
+    h = ALL16[nan].astype(np.uint32)
+    assert_bitexact(dec[nan], (((h & 0x8000) << 16) | 0x7F800000 | ((h & 0x3FF) << 13)).view(np.float32))
+    x = rounding_critical_f32()
+    enc = orc.encode_half(x, 0)
+    isnan = np.isnan(x)
+    with np.errstate(over="ignore"):
+        assert_bitexact(enc[~isnan], x[~isnan].astype(np.float16).view(np.uint16))
+    bits = x[isnan].view(np.uint32)
+    payload = (bits & 0x7FFFFF) >> 13
+    want = ((bits >> 16) & 0x8000) | 0x7C00 | np.where(payload == 0, 1, payload)
+    assert_bitexact(enc[isnan], want.astype(np.uint16))
+
+
+def test_bf16_codec_against_an_independent_rounding(orc):
+    x = rounding_critical_f32()
+    enc = orc.encode_half(x, 1)
+    bits = x.view(np.uint32).astype(np.uint64)
+    # Round half to even at bit 16, written as an explicit decision.
+    low = bits & 0xFFFF
+    up = (low > 0x8000) | ((low == 0x8000) & (((bits >> 16) & 1) == 1))
+    want = ((bits >> 16) + up).astype(np.uint32).astype(np.uint16)
+    isnan = np.isnan(x)
+    assert_bitexact(enc[~isnan], want[~isnan])
+    mant7 = (x[isnan].view(np.uint32) >> 16) & 0x7F
+    want_nan = ((x[isnan].view(np.uint32) >> 16) & 0x8000) | 0x7F80 | np.where(mant7 == 0, 0x40, mant7)
+    assert_bitexact(enc[isnan], want_nan.astype(np.uint16))
+    assert_bitexact(orc.decode_half(ALL16, 1), (ALL16.astype(np.uint32) << 16).view(np.float32))
+
+
+@pytest.mark.parametrize("dt", [0, 1])
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_half_arithmetic_against_numpy(orc, dt, op):
+    rng = np.random.default_rng(3 + dt)
+    a = rng.integers(0, 1 << 16, 1 << 18, dtype=np.uint32).astype(np.uint16)
+    b = rng.integers(0, 1 << 16, 1 << 18, dtype=np.uint32).astype(np.uint16)
+    got = orc.half_binary(a, b, dt, op)
+    x, y = orc.decode_half(a, dt), orc.decode_half(b, dt)
+    with np.errstate(all="ignore"):
+        r = x + y if op == "add" else x * y
+    want = orc.encode_half(r, dt)
+    if dt == 0:
+        with np.errstate(all="ignore"):
+            np_want = r.astype(np.float16).view(np.uint16)
+        ok = ~np.isnan(r)
+        assert_bitexact(want[ok], np_want[ok])
+    assert_bitexact(got, want)
+
+
+def test_half_golden(orc, fx):
+    h = fx["half"]
+    for name, dt in (("f16", 0), ("bf16", 1)):
+        ea, eb = np.array(h[f"{name}_a_bits"], np.uint16), np.array(h[f"{name}_b_bits"], np.uint16)
+        assert_bitexact(orc.encode_half(np.array(h["a"], np.float32), dt), ea)
+        assert_bitexact(orc.half_binary(ea, eb, dt, "add"), np.array(h[f"{name}_add_bits"], np.uint16))
+        assert_bitexact(orc.half_binary(ea, eb, dt, "mul"), np.array(h[f"{name}_mul_bits"], np.uint16))
+
+
+# ---- elementwise -----------------------------------------------------------------
+
+def test_elementwise_are_single_ieee_operations(orc, fx):
+    a = orc.normal(10007, 1, 0.0, 30.0)
+    b = orc.normal(10007, 2, 0.0, 1e-3)
+    assert_bitexact(orc.add(a, b)[0], a + b)
+    assert_bitexact(orc.mul(a, b)[0], a * b)
+    assert_bitexact(orc.mul_scalar(a, b[:1])[0], a * b[0])
+    assert_bitexact(orc.scale(a, 0.125)[0], a * np.float32(0.125))
+    m = a[:7000].reshape(-1, 7)
+    bias = b[:7]
+    assert_bitexact(orc.bias_add(m, bias)[0], m + bias)
+    assert orc.bias_add(a[:10], b[:3])[1] == 1
+    for name in ("add", "mul"):
+        e = fx[name]
+        assert_bitexact(getattr(orc, name)(e["a"], e["b"])[0], np.array(e["expected"], np.float32))
+    e = fx["bias_add"]
+    assert_bitexact(orc.bias_add(e["a"], e["bias"])[0], np.array(e["expected"], np.float32))
+
+
+def test_silu_closed_form(orc, fx):
+    x = orc.normal(100000, 3, 0.0, 6.0)
+    exact = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    assert max_rel_err(orc.silu(x)[0], exact, 1e-37) <= 2.5e-7
+    up = orc.hashed_values(100000, 4)
+    got = orc.silu_mul(x, up)[0]
+    assert max_rel_err(got, exact * up, 1e-37) <= 4e-7
+    special = np.array([0.0, -0.0, 100.0, -100.0, 1e30], np.float32)
+    s = orc.silu(special)[0]
+    assert s[0] == 0.0 and s[2] == np.float32(100.0) and s[4] == np.float32(1e30)
+    assert s[3] == 0.0 and np.signbit(s[3])  # expf overflows: -100 * 0 = -0
+    e = fx["silu"]
+    assert max_rel_err(orc.silu(e["x"])[0], e["expected"], 1e-37) <= e["tolerance"]
+
+
+# ---- embedding --------------------------------------------------------------------
+
+def test_embedding(orc, fx):
+    e = fx["embedding"]
+    out, st = orc.embedding(e["table"], e["ids"])
+    assert st == 0
+    assert_bitexact(out, np.array(e["expected"], np.float32))
+    e = fx["embedding_invalid"]
+    assert orc.embedding(e["table"], e["ids"])[1] == e["expected_status"]
+    table = orc.normal(40, 5).reshape(10, 4)
+    for bad in (-1.0, 1.5, 10.0, np.nan, np.inf, -np.inf, 1e20):
+        assert orc.embedding(table, [bad])[1] == 1, bad
+    out, st = orc.embedding(table, [-0.0, 9.0])
+    assert st == 0
+    assert_bitexact(out, table[[0, 9]])
+
+
+# ---- rmsnorm ----------------------------------------------------------------------
+
+def test_rmsnorm(orc, fx):
+    x = orc.normal(64 * 300, 6).reshape(64, 300)
+    w = orc.normal(300, 7, 1.0, 0.1)
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * w
+    assert max_rel_err(orc.rmsnorm(x, w, 1e-5)[0], exact) <= 2e-6
+    # Constant row c: c / sqrt(c^2 + eps) * w.
+    c = np.full((1, 16), 3.0, np.float32)
+    assert max_rel_err(orc.rmsnorm(c, None, 1e-6)[0], np.full((1, 16), 3.0 / math.sqrt(9 + 1e-6))) <= 2e-7
+    # Per-row weights.
+    wr = orc.normal(64 * 300, 8, 1.0, 0.1).reshape(64, 300)
+    exact_r = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * wr
+    assert max_rel_err(orc.rmsnorm(x, wr, 1e-5, weight_row_stride=300)[0], exact_r) <= 2e-6
+    assert orc.rmsnorm(x, w, 0.0)[1] == 1
+    e = fx["rmsnorm"]
+    assert max_rel_err(orc.rmsnorm(e["x"], e["weight"], e["eps"])[0], e["expected"]) <= e["tolerance"]
+
+
+# ---- softmax -----------------------------------------------------------------------
+
+def test_softmax(orc, fx):
+    x = orc.normal(50 * 1000, 9, 0.0, 2.0).reshape(50, 1000)
+    out, st = orc.softmax_rows(x)
+    assert st == 0
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    assert max_rel_err(out, e / e.sum(axis=1, keepdims=True)) <= 1e-5
+    assert np.max(np.abs(out.astype(np.float64).sum(axis=1) - 1.0)) <= 1e-5
+    shifted, _ = orc.softmax_rows(x + np.float32(3.0))
+    assert max_rel_err(shifted, out) <= 1e-5
+    const, _ = orc.softmax_rows(np.full((2, 8), 5.0, np.float32))
+    assert_bitexact(const, np.full((2, 8), 0.125, np.float32))
+    masked, st = orc.softmax_rows(np.array([[0.0, -np.inf, 0.0]], np.float32))
+    assert st == 0 and masked[0, 1] == 0.0 and masked[0, 0] == 0.5
+    assert orc.softmax_rows(np.full((1, 4), -np.inf, np.float32))[1] == 4
+    f = fx["softmax"]
+    assert max_rel_err(orc.softmax_rows(f["x"])[0], f["expected"]) <= f["tolerance"]
+
+
+# ---- rope -----------------------------------------------------------------------------
+
+def rope64(x, params):
+    x = np.asarray(x, np.float64)
+    rows, cols = x.shape
+    heads, dim = params.head_count, params.dimension
+    hw, half = cols // heads, dim // 2
+    out = x.copy()
+    for r in range(rows):
+        pos = (params.position_offset + r) * params.scale
+        for h in range(heads):
+            for p in range(half):
+                th = pos * params.base ** (-2.0 * p / dim)
+                i1 = h * hw + (p if params.half_split else 2 * p)
+                i2 = h * hw + (p + half if params.half_split else 2 * p + 1)
+                a, b = x[r, i1], x[r, i2]
+                out[r, i1] = a * math.cos(th) - b * math.sin(th)
+                out[r, i2] = a * math.sin(th) + b * math.cos(th)
+    return out
+
+
+def test_rope_reference_fixtures(orc, fx):
+    for e in fx["rope"]:
+        p = orc.rope_params(e["dimension"], e["heads"], base=e["base"], position_offset=e["offset"])
+        out, st = orc.rope(e["x"], p)
+        assert st == 0
+        assert np.max(np.abs(out - np.array(e["expected"], np.float32))) <= e["tolerance"], e["source"]
+
+
+@pytest.mark.parametrize("half_split", [0, 1])
+def test_rope_properties(orc, half_split):
+    x = orc.hashed_values(6 * 96, 10).reshape(6, 96)
+    p = orc.rope_params(16, 4, position_offset=0, half_split=half_split)
+    out, _ = orc.rope(x, p)
+    # Position 0 rotates by 0: row 0 is unchanged.
+    assert_bitexact(out[0], x[0])
+    # Against float64 at small positions; the untouched tail of each head is copied.
+    assert np.max(np.abs(out - rope64(x, p))) <= 1e-6
+    hw = 24
+    for h in range(4):
+        assert_bitexact(out[:, h * hw + 16:(h + 1) * hw], x[:, h * hw + 16:(h + 1) * hw])
+    # Each rotated pair keeps its norm.
+    half = 8
+    xi = x.reshape(6, 4, hw)
+    oi = out.reshape(6, 4, hw)
+    idx1 = np.arange(half) if half_split else 2 * np.arange(half)
+    idx2 = idx1 + half if half_split else idx1 + 1
+    n_in = np.hypot(xi[..., idx1], xi[..., idx2])
+    n_out = np.hypot(oi[..., idx1], oi[..., idx2])
+    assert np.max(np.abs(n_in - n_out)) <= 1e-6
+
+
+def test_rope_pairings_are_a_permutation_of_each_other(orc):
+    """Half-split on x equals interleaved on x with each head's columns permuted
+    so that (p, p + half) become (2p, 2p + 1)."""
+    rows, heads, dim = 5, 3, 8
+    x = orc.hashed_values(rows * heads * dim, 11).reshape(rows, heads * dim)
+    half = dim // 2
+    perm = np.empty(dim, int)
+    perm[0::2] = np.arange(half)
+    perm[1::2] = np.arange(half) + half
+    cols = np.concatenate([h * dim + perm for h in range(heads)])
+    inter, _ = orc.rope(x[:, cols], orc.rope_params(dim, heads, position_offset=7))
+    split, _ = orc.rope(x, orc.rope_params(dim, heads, position_offset=7, half_split=1))
+    back = np.empty_like(inter)
+    back[:, cols] = inter
+    assert_bitexact(split, back)
+
+
+def test_rope_frequency_scaling_bands(orc):
+    base, dim = 500000.0, 16
+    plain, _ = orc.rope_frequencies(orc.rope_params(dim, 1, base=base))
+    banded, _ = orc.rope_frequencies(orc.rope_params(
+        dim, 1, base=base, banded_factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+        original_context_length=64.0))
+    wavelength = 2 * math.pi / plain.astype(np.float64)
+    keep = wavelength < 64 / 4
+    divide = wavelength > 64 / 1
+    assert np.all(banded[keep] == plain[keep])
+    assert max_rel_err(banded[divide], plain[divide] / 8.0) <= 1e-7
+    mid = ~keep & ~divide
+    assert np.all((banded[mid] < plain[mid]) & (banded[mid] > plain[mid] / 8.0))
+    yarn, amp = orc.rope_frequencies(orc.rope_params(dim, 1, base=base, yarn_factor=4.0,
+                                                     yarn_low=2.0, yarn_high=5.0, amplitude=1.25))
+    assert np.all(yarn[:3] == plain[:3])                      # ramp 0 below low
+    assert max_rel_err(yarn[5:], plain[5:] / 4.0) <= 1e-7     # ramp 1 from high
+    assert np.all(amp == np.float32(1.25))
+    part, amp2 = orc.rope_frequencies(orc.rope_params(dim, 1, rotated_pairs=3))
+    assert np.all(part[3:] == 0.0) and np.all(amp2[3:] == 1.0)
+
+
+# ---- matmul ------------------------------------------------------------------------------
+
+def test_matmul_golden_and_exact(orc, fx):
+    e = fx["matmul"]
+    assert_bitexact(orc.matmul(e["a"], e["b"])[0], np.array(e["expected"], np.float32))
+    e = fx["matmul_transposed_a"]
+    assert_bitexact(orc.matmul(e["a"], e["b"], True)[0], np.array(e["expected"], np.float32))
+    rng = np.random.default_rng(1)
+    a = rng.integers(-9, 10, (17, 31)).astype(np.float32)
+    b = rng.integers(-9, 10, (31, 13)).astype(np.float32)
+    exact = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    assert_bitexact(orc.matmul(a, b)[0], exact)
+    assert_bitexact(orc.matmul(a.T.copy(), b, True)[0], exact)
+    assert_bitexact(orc.matmul(a, b.T.copy(), False, True)[0], exact)
+    assert_bitexact(orc.matmul(a.T.copy(), b.T.copy(), True, True)[0], exact)
+    bias = rng.integers(-9, 10, 13).astype(np.float32)
+    assert_bitexact(orc.matmul(a, b, addend=bias, addend_mode=1)[0], exact + bias)
+    assert_bitexact(orc.matmul(a, b, addend=exact, addend_mode=2)[0], exact * 2)
+    assert orc.matmul(a, a)[1] == 1
+
+
+def test_matmul_within_the_summation_bound(orc):
+    """|fl(sum) - sum| <= gamma_k * sum |a||b| for ascending f32 sums (Higham 3.5)."""
+    m, k, n = 40, 777, 30
+    a = orc.uniform(m * k, 12, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 13, -1.0, 1.0).reshape(k, n)
+    got = orc.matmul(a, b)[0].astype(np.float64)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    u = 2.0 ** -24
+    bound = (k * u / (1 - k * u)) * (np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)))
+    assert np.all(np.abs(got - exact) <= bound)
+    rows = orc.matmul_rows(a, b, 5, 9)
+    assert_bitexact(rows, orc.matmul(a, b)[0][5:9])
+
+
+# ---- attention -----------------------------------------------------------------------------
+
+def attention64(q, k, v, seq, kv, H, Hkv, d, causal, window=None):
+    out = np.zeros((seq, H * d))
+    pos = np.arange(kv)
+    for h in range(H):
+        g = h // (H // Hkv)
+        K = k[:, g * d:(g + 1) * d].astype(np.float64)
+        V = v[:, g * d:(g + 1) * d].astype(np.float64)
+        for i in range(seq):
+            qpos = kv - seq + i
+            hi = qpos + 1 if causal else kv
+            lo = max(0, qpos - window + 1) if window else 0
+            m = (pos >= lo) & (pos < hi)
+            s = K[m] @ q[i, h * d:(h + 1) * d].astype(np.float64) / math.sqrt(d)
+            w = np.exp(s - s.max())
+            out[i, h * d:(h + 1) * d] = (w / w.sum()) @ V[m]
+    return out
+
+
+@pytest.mark.parametrize("seq,kv,H,Hkv,d,causal,window", [
+    (1, 300, 12, 2, 16, True, None), (37, 37, 4, 2, 8, True, None), (23, 23, 4, 2, 8, True, 5),
+    (16, 40, 2, 1, 4, False, None), (70, 70, 2, 1, 16, True, 9)])
+def test_attention_against_float64(orc, seq, kv, H, Hkv, d, causal, window):
+    q = orc.attention_values(seq * H * d, 1).reshape(seq, H * d)
+    k = orc.attention_values(kv * Hkv * d, 2).reshape(kv, Hkv * d)
+    v = orc.attention_values(kv * Hkv * d, 3).reshape(kv, Hkv * d)
+    p = orc.attention_params(seq, kv, H, d, kv_head_count=Hkv, causal=causal, window_size=window)
+    out, st = orc.attention(q, k, v, p)
+    assert st == 0
+    assert max_normwise_err(out, attention64(q, k, v, seq, kv, H, Hkv, d, causal, window)) <= 1e-5
+
+
+def test_attention_known_answers(orc, fx):
+    e = fx["attention_large_values"]
+    p = orc.attention_params(1, 4, e["heads"], e["dimension"], causal=e["causal"])
+    out, _ = orc.attention(e["q"], e["k"], e["v"], p)
+    assert np.all(np.isfinite(out))
+    assert np.max(np.abs(out / 1e38 - 1.0)) < e["relative_tolerance"]
+    # Causal query 0 sees key 0 only; a window of 1 sees only its own key.
+    q = orc.hashed_values(5 * 8, 1).reshape(5, 8)
+    k = orc.hashed_values(5 * 8, 2).reshape(5, 8)
+    v = orc.hashed_values(5 * 8, 3).reshape(5, 8)
+    out, _ = orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, causal=True))
+    assert_bitexact(out[0], v[0])
+    out, _ = orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, causal=True, window_size=1))
+    assert_bitexact(out, v)
+    # Identical keys: uniform weights, the mean of the admitted V rows.
+    kk = np.tile(k[:1], (5, 1))
+    out, _ = orc.attention(q, kk, v, orc.attention_params(5, 5, 2, 4, causal=False))
+    assert max_normwise_err(out, np.tile(v.astype(np.float64).mean(axis=0), (5, 1))) <= 1e-6
+    # Validation mirrors src/kernels.rs:6533-6620.
+    assert orc.attention(q, k, v, orc.attention_params(5, 5, 3, 4, kv_head_count=2))[1] == 1
+    assert orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, window_size=2))[1] == 1
+    assert orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, key_count=4))[1] == 1
