@@ -39,10 +39,12 @@ def seed(config: int, tensor: int) -> int:
 
 
 class Case:
-    """One kernel at one shape: `launch()` enqueues exactly one call."""
+    """One kernel at one shape: `launch()` enqueues exactly one call.
+    `tokens`, when set, also reports tokens/s (the decoder-block chains)."""
 
-    def __init__(self, name, launch, work, bound, shape):
+    def __init__(self, name, launch, work, bound, shape, tokens=None):
         self.name, self.launch, self.work, self.bound, self.shape = name, launch, work, bound, shape
+        self.tokens = tokens
 
     def measure(self, dev, steps, warmup):
         for _ in range(warmup):
@@ -58,9 +60,12 @@ class Case:
         else:
             achieved = self.work / (ms * 1e-3) / 1e12
             peak, unit = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
-        return {"ms": ms, "achieved": achieved, "unit": unit, "peak": peak,
-                "frac": achieved / peak, "work": self.work, "bound": self.bound,
-                "shape": self.shape}
+        out = {"ms": ms, "achieved": achieved, "unit": unit, "peak": peak,
+               "frac": achieved / peak, "work": self.work, "bound": self.bound,
+               "shape": self.shape}
+        if self.tokens:
+            out["tokens_per_s"] = self.tokens / (ms * 1e-3)
+        return out
 
 
 def streaming_cases(dev, orc):
@@ -153,6 +158,59 @@ def attention_cases(dev, orc):
     return cases
 
 
+def _device_normal(dev, shape, s, std):
+    """A seeded N(0, std) device tensor, generated on the host in chunks."""
+    import ctypes
+    from oracle import oracle as orc
+    from magnetar_hip._lib import call
+    arr = dev.empty(shape)
+    n = int(np.prod(shape))
+    chunk = 16 << 20
+    for i0 in range(0, n, chunk):
+        host = orc.normal(min(chunk, n - i0), s + i0, 0.0, std)
+        call("mhip_upload", dev.ctx, ctypes.c_void_p(arr.ptr + 4 * i0),
+             host.ctypes.data_as(ctypes.c_void_p), host.nbytes)
+    return arr
+
+
+def decoder_cases(dev, orc):
+    """The chained decoder block: config 0 (tiny, seq 32) and config 4
+    (Llama-2-7B shapes: prefill 512, decode one token at KV 2048)."""
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    cases = []
+
+    def block(shapes, cfg, cache_rows, max_seq):
+        w = {}
+        for i, (name, shape) in enumerate(shapes.weight_shapes().items()):
+            if name.endswith("norm"):
+                w[name] = dev.upload(np.ones(shape, np.float32))
+            else:
+                w[name] = _device_normal(dev, shape, seed(cfg, 16 + i), 0.02)
+        return DecoderBlock(dev, shapes, w, cache_rows=cache_rows, max_seq=max_seq)
+
+    tiny = Shapes(vocab=1024, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=688)
+    b0 = block(tiny, 0, 32, 32)
+    ids0 = dev.upload(orc.token_ids(32, seed(0, 1), 1024))
+    out0 = dev.empty((32, 256))
+    w0 = 4 * (4 * 256 * 256 + 3 * 256 * 688)
+    cases.append(Case("decoder_c1_seq32", lambda: b0.forward(ids0, 0, out0), w0, "hbm",
+                      [32, 256], tokens=32))
+    big = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
+    b4 = block(big, 4, 2049, 512)
+    ids_p = dev.upload(orc.token_ids(512, seed(4, 8), 32000))
+    out_p = dev.empty((512, 4096))
+    flops = 2.0 * 512 * (4 * 4096 * 4096 + 3 * 4096 * 11008) + 4.0 * 128 * 512 * 513 / 2 * 32
+    cases.append(Case("decoder_c5_prefill512", lambda: b4.forward(ids_p, 0, out_p), flops, "mfma",
+                      [512, 4096], tokens=512))
+    ids_d = dev.upload(orc.token_ids(1, seed(4, 9), 32000))
+    out_d = dev.empty((1, 4096))
+    weight_bytes = 4 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
+    kv_bytes = 2 * 2049 * 4096 * 4
+    cases.append(Case("decoder_c5_decode_kv2048", lambda: b4.forward(ids_d, 2048, out_d),
+                      weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
+    return cases
+
+
 def cpu_baseline(orc, budget_s=12.0):
     """The oracle's matmul (f32, k ascending, one thread) on whole rows of the
     4096^3 headline product, as many rows as fit the time budget."""
@@ -207,7 +265,8 @@ def main(argv=None):
 
     dev = magnetar_hip.Device(0)
     info = dev.info()
-    cases = matmul_cases(dev, orc) + attention_cases(dev, orc) + streaming_cases(dev, orc)
+    cases = (matmul_cases(dev, orc) + attention_cases(dev, orc) + streaming_cases(dev, orc)
+             + decoder_cases(dev, orc))
     only = set(filter(None, args.only.split(",")))
     results = {}
     for case in cases:
@@ -215,8 +274,9 @@ def main(argv=None):
             continue
         results[case.name] = case.measure(dev, args.steps, args.warmup)
         r = results[case.name]
+        extra = f"  {r['tokens_per_s']:10.1f} tokens/s" if "tokens_per_s" in r else ""
         print(f"# {case.name:14s} {r['ms']*1e3:9.1f} us  {r['achieved']:8.1f} {r['unit']}  "
-              f"{100*r['frac']:5.1f}% of {r['bound']}", file=sys.stderr, flush=True)
+              f"{100*r['frac']:5.1f}% of {r['bound']}{extra}", file=sys.stderr, flush=True)
     dev.check_flags()
 
     head = results.get(HEADLINE)
@@ -245,8 +305,10 @@ def main(argv=None):
         "cpu_baseline": base,
         "device": {"name": info["name"], "arch": info["architecture"],
                    "compute_units": info["compute_units"]},
-        "kernels": {k: {"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),
-                        "unit": v["unit"], "frac": round(v["frac"], 4), "shape": v["shape"]}
+        "kernels": {k: dict({"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),
+                             "unit": v["unit"], "frac": round(v["frac"], 4), "shape": v["shape"]},
+                            **({"tokens_per_s": round(v["tokens_per_s"], 1)}
+                               if "tokens_per_s" in v else {}))
                     for k, v in results.items()},
     }
     print(json.dumps(line))

@@ -215,6 +215,49 @@ typedef struct {
 mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
                                float* out, const mhip_attention_params* params);
 
+/* ---- decoder block, chained device-resident (src/tests_hardware_hot_path.rs:339-526) ---- */
+typedef struct {
+    uint64_t hidden;            /* = heads * head_dim */
+    uint64_t heads;
+    uint64_t kv_heads;
+    uint64_t head_dim;
+    uint64_t ffn;               /* SwiGLU intermediate width */
+    uint64_t vocab;
+    float eps;                  /* RMSNorm epsilon */
+    float rope_base;            /* RoPE theta */
+} mhip_block_config;
+
+/* Device pointers, all f32 row-major: embedding [vocab, hidden]; attn_norm and
+ * ffn_norm [hidden]; wq [hidden, H*hd], wk and wv [hidden, Hkv*hd],
+ * wo [H*hd, hidden]; w_gate and w_up [hidden, ffn]; w_down [ffn, hidden]. */
+typedef struct {
+    const float* embedding;
+    const float* attn_norm;
+    const float* wq;
+    const float* wk;
+    const float* wv;
+    const float* wo;
+    const float* ffn_norm;
+    const float* w_gate;
+    const float* w_up;
+    const float* w_down;
+} mhip_block_weights;
+
+/* Workspace bytes mhip_block_forward needs for `seq` tokens. */
+uint64_t mhip_block_workspace_bytes(const mhip_block_config* cfg, uint64_t seq);
+/* One block over `seq` tokens (ids: f32 token ids on the device) at positions
+ * position .. position+seq-1: embedding -> rmsnorm -> q/k/v -> rope ->
+ * K/V written into cache rows [position, position+seq) -> causal attention over
+ * position+seq keys -> o-proj + residual -> rmsnorm -> silu(gate) * up ->
+ * down + residual -> out [seq, hidden]. k_cache / v_cache: [cache_rows,
+ * kv_heads*head_dim]. Enqueues only; an invalid id is reported by
+ * mhip_check_flags. */
+mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
+                               const mhip_block_weights* weights, const float* ids, uint64_t seq,
+                               uint64_t position, float* k_cache, float* v_cache,
+                               uint64_t cache_rows, void* workspace, uint64_t workspace_bytes,
+                               float* out);
+
 /* ======================================================================== */
 /* Executor: the `CudaExecutor`-shaped ProviderExecutionApi (src/executor.rs) */
 /* ======================================================================== */

@@ -1,0 +1,117 @@
+// A Llama-style decoder block chained device-resident over the C ABI's
+// Kernels, with an in-place KV cache.
+//
+// The reference composes this chain in the Runtime (no single function;
+// closest: src/tests_hardware_hot_path.rs:339-526 and
+// benches/kernel_chaining.rs:59-89): embedding -> rmsnorm -> Q/K/V matmuls ->
+// rope (Q with H heads, K with Hkv heads) -> causal attention -> output matmul
+// + residual -> rmsnorm -> gate/up matmuls -> silu * up -> down matmul +
+// residual. Decode appends K/V rows at `position` (`kv-write`,
+// src/kernels.rs:2278-2325) and attends to `position + seq` keys
+// (`key_count`). Here the K and V projections are written straight into
+// their cache rows and rotated in place, so the append costs no copy, and the
+// residual adds ride in the matmul epilogues (matmul-residual, bit-identical
+// to matmul + add). All launches go on the context's stream; nothing waits.
+#include <cstring>
+#include <string>
+
+#include "magnetar_hip.h"
+
+namespace {
+
+struct Layout {
+    uint64_t x, h, q, a, x2, h2, g, u;  // float offsets into the workspace
+    uint64_t floats;
+};
+
+Layout layout(const mhip_block_config& c, uint64_t seq) {
+    Layout l{};
+    uint64_t off = 0;
+    auto take = [&](uint64_t n) {
+        uint64_t at = off;
+        off += (n + 63) / 64 * 64;  // 256-byte aligned slices
+        return at;
+    };
+    l.x = take(seq * c.hidden);
+    l.h = take(seq * c.hidden);
+    l.q = take(seq * c.heads * c.head_dim);
+    l.a = take(seq * c.heads * c.head_dim);
+    l.x2 = take(seq * c.hidden);
+    l.h2 = take(seq * c.hidden);
+    l.g = take(seq * c.ffn);
+    l.u = take(seq * c.ffn);
+    l.floats = off;
+    return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t mhip_block_workspace_bytes(const mhip_block_config* cfg, uint64_t seq) {
+    if (!cfg) return 0;
+    return layout(*cfg, seq).floats * sizeof(float);
+}
+
+mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
+                               const mhip_block_weights* w, const float* ids, uint64_t seq,
+                               uint64_t position, float* k_cache, float* v_cache,
+                               uint64_t cache_rows, void* workspace, uint64_t workspace_bytes,
+                               float* out) {
+    if (!ctx) return MHIP_DEVICE_UNAVAILABLE;
+    if (!cfg || !w || !ids || !k_cache || !v_cache || !workspace || !out)
+        return MHIP_SHAPE_UNSUPPORTED;
+    const mhip_block_config& c = *cfg;
+    if (c.heads == 0 || c.kv_heads == 0 || c.heads % c.kv_heads != 0 || c.head_dim == 0 ||
+        c.heads * c.head_dim != c.hidden || seq == 0 || position + seq > cache_rows)
+        return MHIP_SHAPE_UNSUPPORTED;
+    const Layout l = layout(c, seq);
+    if (workspace_bytes < l.floats * sizeof(float)) return MHIP_SHAPE_UNSUPPORTED;
+    float* ws = static_cast<float*>(workspace);
+    float *x = ws + l.x, *h = ws + l.h, *q = ws + l.q, *a = ws + l.a, *x2 = ws + l.x2,
+          *h2 = ws + l.h2, *g = ws + l.g, *u = ws + l.u;
+    const uint64_t kv_dim = c.kv_heads * c.head_dim;
+    float* k_rows = k_cache + position * kv_dim;
+    float* v_rows = v_cache + position * kv_dim;
+    mhip_status st;
+#define MHIP_TRY(call)                 \
+    do {                               \
+        if ((st = (call)) != MHIP_OK) \
+            return st;                 \
+    } while (0)
+    MHIP_TRY(mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
+    MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
+    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, 0, 0, nullptr, 0));
+    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wk, k_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
+    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wv, v_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
+    mhip_rope_params rp;
+    mhip_rope_params_default(&rp, c.head_dim, c.heads);
+    rp.base = c.rope_base;
+    rp.position_offset = position;
+    MHIP_TRY(mhip_rope_f32(ctx, q, q, seq, c.heads * c.head_dim, &rp));
+    rp.head_count = c.kv_heads;
+    MHIP_TRY(mhip_rope_f32(ctx, k_rows, k_rows, seq, kv_dim, &rp));
+    mhip_attention_params ap;
+    std::memset(&ap, 0, sizeof(ap));
+    ap.seq_len = seq;
+    ap.kv_rows = cache_rows;
+    ap.kv_seq_len = position + seq;
+    ap.head_count = c.heads;
+    ap.kv_head_count = c.kv_heads;
+    ap.head_dimension = c.head_dim;
+    ap.value_dimension = c.head_dim;
+    ap.causal = 1;
+    ap.window_size = -1;
+    ap.batch = 1;
+    MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
+    MHIP_TRY(mhip_matmul_f32(ctx, a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, 0, 0, x, 2));
+    MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
+    MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_gate, g, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
+    MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_up, u, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
+    MHIP_TRY(mhip_silu_mul_f32(ctx, g, u, g, seq * c.ffn));
+    MHIP_TRY(mhip_matmul_f32(ctx, g, w->w_down, out, seq, c.ffn, c.hidden, 0, 0, x2, 2));
+#undef MHIP_TRY
+    return MHIP_OK;
+}
+
+}  // extern "C"

@@ -418,13 +418,24 @@ int orc_matmul(const float* a, const float* b, float* out, uint64_t m, uint64_t 
                int addend_mode) {
     uint64_t a_row = transpose_a ? 1 : k, a_inner = transpose_a ? m : 1;
     uint64_t b_inner = transpose_b ? 1 : n, b_col = transpose_b ? k : 1;
+    /* Loop-interchanged so B streams by rows: every out[r][c] still starts at
+     * 0.0f and adds a[r][i] * b[i][c] for i ascending, one f32 rounding each. */
     for (uint64_t r = 0; r < m; r++) {
-        for (uint64_t c = 0; c < n; c++) {
-            float acc = 0.0f;
-            for (uint64_t i = 0; i < k; i++) acc += a[r * a_row + i * a_inner] * b[i * b_inner + c * b_col];
-            if (addend_mode == 1) acc = acc + addend[c];
-            else if (addend_mode == 2) acc = acc + addend[r * n + c];
-            out[r * n + c] = acc;
+        float* o = out + r * n;
+        for (uint64_t c = 0; c < n; c++) o[c] = 0.0f;
+        for (uint64_t i = 0; i < k; i++) {
+            float av = a[r * a_row + i * a_inner];
+            const float* brow = b + i * b_inner;
+            if (b_col == 1) {
+                for (uint64_t c = 0; c < n; c++) o[c] += av * brow[c];
+            } else {
+                for (uint64_t c = 0; c < n; c++) o[c] += av * brow[c * b_col];
+            }
+        }
+        if (addend_mode == 1) {
+            for (uint64_t c = 0; c < n; c++) o[c] = o[c] + addend[c];
+        } else if (addend_mode == 2) {
+            for (uint64_t c = 0; c < n; c++) o[c] = o[c] + addend[r * n + c];
         }
     }
     return ORC_OK;

@@ -38,8 +38,8 @@ def test_library_exports_every_declared_function():
 
 
 def test_python_bindings_cover_the_abi():
-    from magnetar_hip import _lib, executor
-    bound = set(_lib.SIGNATURES) | set(executor._SIGS)
+    from magnetar_hip import _lib, executor, decoder
+    bound = set(_lib.SIGNATURES) | set(executor._SIGS) | set(decoder.SIGNATURES)
     assert set(declared_functions()) <= bound
 
 
