@@ -31,7 +31,7 @@ MB = 1e6
 HEADLINE = "matmul_4096"
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
 # scaled by a plain copy's reading); null until measured.
-TRAFFIC: dict = {}
+TRAFFIC: dict = {"matmul_4096": 852_837_000}  # profiles/matmul_4096_mfma_gemm.md
 
 
 def seed(config: int, tensor: int) -> int:
@@ -113,6 +113,17 @@ def streaming_cases(dev, orc):
                                ops.half_binary(dev, ha, hb, op, dt, ho)),
                               3 * hn * 2, "hbm", [hn]))
     return cases
+
+
+def calibration_cases(dev, orc):
+    """A plain copy of known size (scale by 1.0 over 64M floats: 268 MB read,
+    268 MB written), run only when named: it calibrates the rocprofv3
+    FETCH_SIZE / WRITE_SIZE counters against bytes that are known."""
+    from magnetar_hip import ops
+    n = 1 << 26
+    x = dev.upload(orc.normal(n, seed(9, 0)))
+    y = dev.empty((n,))
+    return [Case("calibration_copy", lambda: ops.scale(dev, x, 1.0, y), 2 * n * 4, "hbm", [n])]
 
 
 def matmul_cases(dev, orc):
@@ -265,9 +276,20 @@ def main(argv=None):
 
     dev = magnetar_hip.Device(0)
     info = dev.info()
-    cases = (matmul_cases(dev, orc) + attention_cases(dev, orc) + streaming_cases(dev, orc)
-             + decoder_cases(dev, orc))
     only = set(filter(None, args.only.split(",")))
+    wanted = lambda prefix: not only or any(name.startswith(prefix) for name in only)
+    cases = []
+    if wanted("matmul"):
+        cases += matmul_cases(dev, orc)
+    if wanted("attention"):
+        cases += attention_cases(dev, orc)
+    if not only or only - {c for c in only if c.startswith(("matmul", "attention", "decoder",
+                                                             "calibration"))}:
+        cases += streaming_cases(dev, orc)
+    if wanted("decoder"):
+        cases += decoder_cases(dev, orc)
+    if any(name.startswith("calibration") for name in only):
+        cases += calibration_cases(dev, orc)
     results = {}
     for case in cases:
         if only and case.name not in only:
