@@ -47,12 +47,12 @@ class Case:
         self.tokens = tokens
 
     def measure(self, dev, steps, warmup):
-        for _ in range(warmup):
-            self.launch()
+        for i in range(warmup):
+            self.launch(i)
         dev.sync()
         dev.timer_start()
-        for _ in range(steps):
-            self.launch()
+        for i in range(steps):
+            self.launch(warmup + i)
         ms = dev.timer_stop() / steps
         if self.bound == "hbm":
             achieved = self.work / (ms * 1e-3) / 1e9
@@ -68,49 +68,68 @@ class Case:
         return out
 
 
+# MI355X's 256 MB Infinity Cache would hold a whole working set of the
+# bandwidth cases between repeated launches; each such case cycles through
+# enough copies of its tensors (>= 1 GB) that every launch reads and writes
+# HBM, as a single pass over fresh data does.
+CACHE_ROTATION_BYTES = 1 << 30
+
+
+def _copies(footprint):
+    return max(1, -(-CACHE_ROTATION_BYTES // footprint))
+
+
 def streaming_cases(dev, orc):
     from magnetar_hip import ops, MHIP_F16, MHIP_BF16
     cases = []
     rows, cols = 8192, 4096
     n = rows * cols
-    x = dev.upload(orc.normal(n, seed(3, 0)))
-    y = dev.upload(orc.normal(n, seed(3, 1)))
-    out = dev.empty((n,))
-    gain = dev.upload(orc.normal(cols, seed(3, 2), 1.0, 0.1))
     f32 = 4
-    cases.append(Case("add", lambda: ops.add(dev, x, y, out), 3 * n * f32, "hbm", [n]))
-    cases.append(Case("mul", lambda: ops.mul(dev, x, y, out), 3 * n * f32, "hbm", [n]))
-    cases.append(Case("residual_add", lambda: ops.add(dev, x, y, out), 3 * n * f32, "hbm", [n]))
-    cases.append(Case("silu", lambda: ops.silu(dev, x, out), 2 * n * f32, "hbm", [n]))
-    cases.append(Case("silu_mul", lambda: ops.silu_mul(dev, x, y, out), 3 * n * f32, "hbm", [n]))
-    x2 = _reshape(x, (rows, cols))
-    o2 = _reshape(out, (rows, cols))
-    cases.append(Case("rmsnorm", lambda: ops.rmsnorm(dev, x2, gain, 1e-5, out=o2),
+    r3, r2 = _copies(3 * n * f32), _copies(2 * n * f32)
+    xs = [dev.upload(orc.normal(n, seed(3, 10 + i))) for i in range(max(r3, r2))]
+    ys = [dev.upload(orc.normal(n, seed(3, 20 + i))) for i in range(r3)]
+    outs = [dev.empty((n,)) for _ in range(max(r3, r2))]
+    gain = dev.upload(orc.normal(cols, seed(3, 2), 1.0, 0.1))
+    cases.append(Case("add", lambda i: ops.add(dev, xs[i % r3], ys[i % r3], outs[i % r3]),
+                      3 * n * f32, "hbm", [n]))
+    cases.append(Case("mul", lambda i: ops.mul(dev, xs[i % r3], ys[i % r3], outs[i % r3]),
+                      3 * n * f32, "hbm", [n]))
+    cases.append(Case("residual_add", lambda i: ops.add(dev, xs[i % r3], ys[i % r3], outs[i % r3]),
+                      3 * n * f32, "hbm", [n]))
+    cases.append(Case("silu", lambda i: ops.silu(dev, xs[i % r2], outs[i % r2]), 2 * n * f32,
+                      "hbm", [n]))
+    cases.append(Case("silu_mul", lambda i: ops.silu_mul(dev, xs[i % r3], ys[i % r3], outs[i % r3]),
+                      3 * n * f32, "hbm", [n]))
+    x2 = [_reshape(x, (rows, cols)) for x in xs]
+    o2 = [_reshape(o, (rows, cols)) for o in outs]
+    cases.append(Case("rmsnorm", lambda i: ops.rmsnorm(dev, x2[i % r2], gain, 1e-5, out=o2[i % r2]),
                       2 * n * f32 + cols * f32, "hbm", [rows, cols]))
-    sm_in = dev.upload(orc.normal(n, seed(3, 3), 0.0, 2.0).reshape(rows, cols))
-    cases.append(Case("softmax", lambda: ops.softmax_rows(dev, sm_in, out=o2),
+    sm = [dev.upload(orc.normal(n, seed(3, 30 + i), 0.0, 2.0).reshape(rows, cols)) for i in range(r2)]
+    cases.append(Case("softmax", lambda i: ops.softmax_rows(dev, sm[i % r2], out=o2[i % r2]),
                       2 * n * f32, "hbm", [rows, cols]))
     rp = ops.rope_params(128, 32)
-    cases.append(Case("rope", lambda: ops.rope(dev, x2, rp, out=o2), 2 * n * f32, "hbm",
-                      [rows, 32 * 128]))
+    cases.append(Case("rope", lambda i: ops.rope(dev, x2[i % r2], rp, out=o2[i % r2]), 2 * n * f32,
+                      "hbm", [rows, 32 * 128]))
     # Embedding: 8192 ids into a [128000, 4096] table (2.1 GB resident).
     vocab = 128000
     table = dev.empty((vocab, cols))
     _fill_normal(dev, table, seed(3, 4))
-    ids = dev.upload(orc.token_ids(8192, seed(3, 5), vocab))
-    emb_out = dev.empty((8192, cols))
-    cases.append(Case("embedding", lambda: ops.embedding(dev, table, ids, emb_out),
+    re = _copies(2 * 8192 * cols * f32)
+    ids = [dev.upload(orc.token_ids(8192, seed(3, 50 + i), vocab)) for i in range(re)]
+    emb_out = [dev.empty((8192, cols)) for _ in range(re)]
+    cases.append(Case("embedding", lambda i: ops.embedding(dev, table, ids[i % re], emb_out[i % re]),
                       2 * 8192 * cols * f32 + 8192 * f32, "hbm", [8192, cols]))
     # Half path: 64M elements per tensor.
     hn = 1 << 26
+    rh = _copies(3 * hn * 2)
     for dname, dt in (("f16", MHIP_F16), ("bf16", MHIP_BF16)):
-        ha = dev.upload(orc.encode_half(orc.normal(hn, seed(3, 6)), dt), half=dt)
-        hb = dev.upload(orc.encode_half(orc.normal(hn, seed(3, 7)), dt), half=dt)
-        ho = dev.empty((hn,), np.uint16, dt)
+        ha = [dev.upload(orc.encode_half(orc.normal(hn, seed(3, 60 + i)), dt), half=dt) for i in range(rh)]
+        hb = [dev.upload(orc.encode_half(orc.normal(hn, seed(3, 70 + i)), dt), half=dt) for i in range(rh)]
+        ho = [dev.empty((hn,), np.uint16, dt) for _ in range(rh)]
         for op in ("add", "mul"):
             cases.append(Case(f"{op}_{dname}",
-                              (lambda ha=ha, hb=hb, ho=ho, op=op, dt=dt:
-                               ops.half_binary(dev, ha, hb, op, dt, ho)),
+                              (lambda i, ha=ha, hb=hb, ho=ho, op=op, dt=dt:
+                               ops.half_binary(dev, ha[i % rh], hb[i % rh], op, dt, ho[i % rh])),
                               3 * hn * 2, "hbm", [hn]))
     return cases
 
@@ -123,7 +142,7 @@ def calibration_cases(dev, orc):
     n = 1 << 26
     x = dev.upload(orc.normal(n, seed(9, 0)))
     y = dev.empty((n,))
-    return [Case("calibration_copy", lambda: ops.scale(dev, x, 1.0, y), 2 * n * 4, "hbm", [n])]
+    return [Case("calibration_copy", lambda i: ops.scale(dev, x, 1.0, y), 2 * n * 4, "hbm", [n])]
 
 
 def matmul_cases(dev, orc):
@@ -133,12 +152,14 @@ def matmul_cases(dev, orc):
         a = dev.upload(orc.uniform(size * size, seed(2, size), -1.0, 1.0).reshape(size, size))
         b = dev.upload(orc.uniform(size * size, seed(2, size + 1), -1.0, 1.0).reshape(size, size))
         c = dev.empty((size, size))
-        cases.append(Case(f"matmul_{size}", (lambda a=a, b=b, c=c: ops.matmul(dev, a, b, out=c)),
+        cases.append(Case(f"matmul_{size}", (lambda i, a=a, b=b, c=c: ops.matmul(dev, a, b, out=c)),
                           2.0 * size ** 3, "mfma", [size, size, size]))
     a = dev.upload(orc.uniform(4096, seed(2, 1), -1.0, 1.0).reshape(1, 4096))
-    b = dev.upload(orc.uniform(4096 * 11008, seed(2, 2), -1.0, 1.0).reshape(4096, 11008))
+    rb = _copies(4096 * 11008 * 4)
+    bs = [dev.upload(orc.uniform(4096 * 11008, seed(2, 2 + i), -1.0, 1.0).reshape(4096, 11008))
+          for i in range(rb)]
     c = dev.empty((1, 11008))
-    cases.append(Case("matmul_1x4096x11008", lambda: ops.matmul(dev, a, b, out=c),
+    cases.append(Case("matmul_1x4096x11008", lambda i: ops.matmul(dev, a, bs[i % rb], out=c),
                       4 * (4096 * 11008 + 4096 + 11008), "hbm", [1, 4096, 11008]))
     return cases
 
@@ -153,7 +174,7 @@ def attention_cases(dev, orc):
     o = dev.empty((B * S, H * d))
     p = ops.attention_params(S, S, H, d, causal=True, batch=B)
     flops = 4.0 * d * S * (S + 1) / 2 * B * H
-    cases.append(Case("attention_prefill", lambda: ops.attention(dev, q, k, v, p, o), flops,
+    cases.append(Case("attention_prefill", lambda i: ops.attention(dev, q, k, v, p, o), flops,
                       "mfma", [B, H, S, d]))
     B2, KV = 8, 4096
     q2 = dev.upload(orc.normal(B2 * H * d, seed(4, 3)).reshape(B2, H * d))
@@ -164,7 +185,7 @@ def attention_cases(dev, orc):
     o2 = dev.empty((B2, H * d))
     p2 = ops.attention_params(1, KV, H, d, causal=True, batch=B2)
     nbytes = 2 * B2 * KV * H * d * 4 + 2 * B2 * H * d * 4
-    cases.append(Case("attention_decode", lambda: ops.attention(dev, q2, k2, v2, p2, o2), nbytes,
+    cases.append(Case("attention_decode", lambda i: ops.attention(dev, q2, k2, v2, p2, o2), nbytes,
                       "hbm", [B2, H, KV, d]))
     return cases
 
@@ -204,20 +225,20 @@ def decoder_cases(dev, orc):
     ids0 = dev.upload(orc.token_ids(32, seed(0, 1), 1024))
     out0 = dev.empty((32, 256))
     w0 = 4 * (4 * 256 * 256 + 3 * 256 * 688)
-    cases.append(Case("decoder_c1_seq32", lambda: b0.forward(ids0, 0, out0), w0, "hbm",
+    cases.append(Case("decoder_c1_seq32", lambda i: b0.forward(ids0, 0, out0), w0, "hbm",
                       [32, 256], tokens=32))
     big = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     b4 = block(big, 4, 2049, 512)
     ids_p = dev.upload(orc.token_ids(512, seed(4, 8), 32000))
     out_p = dev.empty((512, 4096))
     flops = 2.0 * 512 * (4 * 4096 * 4096 + 3 * 4096 * 11008) + 4.0 * 128 * 512 * 513 / 2 * 32
-    cases.append(Case("decoder_c5_prefill512", lambda: b4.forward(ids_p, 0, out_p), flops, "mfma",
+    cases.append(Case("decoder_c5_prefill512", lambda i: b4.forward(ids_p, 0, out_p), flops, "mfma",
                       [512, 4096], tokens=512))
     ids_d = dev.upload(orc.token_ids(1, seed(4, 9), 32000))
     out_d = dev.empty((1, 4096))
     weight_bytes = 4 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
     kv_bytes = 2 * 2049 * 4096 * 4
-    cases.append(Case("decoder_c5_decode_kv2048", lambda: b4.forward(ids_d, 2048, out_d),
+    cases.append(Case("decoder_c5_decode_kv2048", lambda i: b4.forward(ids_d, 2048, out_d),
                       weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
     return cases
 

@@ -32,6 +32,21 @@ struct mhip_ctx {
 
 namespace mhip {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming outputs: a non-temporal dwordx4 store, which skips allocating the
+// line in L2 (each output is written once and read, if at all, by a later
+// launch).
+__device__ __forceinline__ void store_nt(float4* p, float4 v) {
+    f32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
+}
+__device__ __forceinline__ void store_nt(uint4* p, uint4 v) {
+    u32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
+}
+
 // Records `detail` as this thread's last error and returns `status`.
 mhip_status fail(mhip_status status, const std::string& detail);
 // Maps a HIP runtime error onto the stable categories (src/error.rs:71-91).

@@ -4,6 +4,9 @@
 // covers the tensor with >= 256 threads x 64 bytes per workgroup, far more
 // workgroups than the 256 CUs at the benchmark sizes.
 //
+// Outputs are written with non-temporal stores (no L2 allocation for data
+// written once).
+//
 // Semantics follow the reference kernels one element at a time
 // (src/kernels.cu:30-117, :1091-1096); the vector width changes nothing in
 // the arithmetic, so add/mul/bias-add/scale are bit-identical to the CPU
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(kThreads) void binary_kernel(const float* __restric
     for (int u = 0; u < kUnroll; ++u) {
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
         if (i < full) {
-            o4[i] = apply2(op, va[u], vb[u]);
+            mhip::store_nt(o4 + i, apply2(op, va[u], vb[u]));
         } else if (i == full) {
             for (uint64_t e = full * 4; e < n; ++e) out[e] = op(a[e], b[e]);
         }
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void unary_kernel(const float* __restrict
     for (int u = 0; u < kUnroll; ++u) {
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
         if (i < full) {
-            o4[i] = apply1(op, vx[u]);
+            mhip::store_nt(o4 + i, apply1(op, vx[u]));
         } else if (i == full) {
             for (uint64_t e = full * 4; e < n; ++e) out[e] = op(x[e]);
         }
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void mul_scalar_kernel(const float* __res
     for (int u = 0; u < kUnroll; ++u) {
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
         if (i < full) {
-            o4[i] = make_float4(va[u].x * s, va[u].y * s, va[u].z * s, va[u].w * s);
+            mhip::store_nt(o4 + i, make_float4(va[u].x * s, va[u].y * s, va[u].z * s, va[u].w * s));
         } else if (i == full) {
             for (uint64_t e = full * 4; e < n; ++e) out[e] = a[e] * s;
         }
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void bias_add_vec_kernel(const float* __r
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-        if (i < n4) o4[i] = apply2(AddOp{}, va[u], vb[u]);
+        if (i < n4) mhip::store_nt(o4 + i, apply2(AddOp{}, va[u], vb[u]));
     }
 }
 

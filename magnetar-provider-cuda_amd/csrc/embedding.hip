@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void embedding_vec_kernel(
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             uint64_t c = c0 + static_cast<uint64_t>(u) * TPR;
-            if (c < dim4) dst[c] = v[u];
+            if (c < dim4) mhip::store_nt(dst + c, v[u]);
         }
     }
 }

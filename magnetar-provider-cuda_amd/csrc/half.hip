@@ -12,7 +12,8 @@
 //  - f16 encode uses v_cvt_f16_f32 (round-to-nearest-even, overflow to inf,
 //    subnormal results rounded) and applies the reference's NaN payload rule;
 //  - bf16 is the reference's integer rounding itself (bits + 0x7FFF + lsb).
-// Each thread moves 8 halves per 16-byte access.
+// Each thread moves 8 halves per 16-byte access; outputs use non-temporal
+// stores.
 #include "common.hpp"
 
 namespace {
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void half_binary_kernel(const uint16_t* _
             r.y = op2<DT, OP>(va[u].y, vb[u].y);
             r.z = op2<DT, OP>(va[u].z, vb[u].z);
             r.w = op2<DT, OP>(va[u].w, vb[u].w);
-            o4[i] = r;
+            mhip::store_nt(o4 + i, r);
         } else if (i == full) {
             for (uint64_t e = full * 8; e < n; ++e)
                 out[e] = static_cast<uint16_t>(op1<DT, OP>(a[e], b[e]));

@@ -21,7 +21,8 @@
 //  - m <= kGemvMaxRows (decode): the work is reading B once (HBM-bound), so
 //    each wave streams 256 columns of B with dwordx4 loads over one k slice,
 //    keeping m x 4 partial sums per lane; partial sums per k slice go to a
-//    workspace and a second pass adds them in slice order (deterministic).
+//    workspace and a second launch adds them in a fixed order
+//    (deterministic), four waves per 256 columns.
 #include "common.hpp"
 
 namespace {
@@ -254,22 +255,25 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c,
 constexpr int kGemvThreads = 256;
 constexpr int kGemvCols = 256;  // columns per workgroup: 64 lanes x 4
 
-// Workgroup (column group x, k slice y): its 4 waves split the slice's rows,
-// then sum in LDS; partial[y][row][col] receives the slice's sum.
+// Workgroup (column group x, k slice y): its 4 waves split the slice's rows
+// and meet in LDS. With one slice it writes C (+ addend) itself; otherwise it
+// writes the slice's partial sums for gemv_reduce_kernel.
 template <int ROWS>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ partial,
-    uint64_t K, uint64_t N, uint64_t k_per_slice) {
-    __shared__ float4 red[3][ROWS][64];
+    float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
+    const float* __restrict__ addend, int addend_mode) {
+    __shared__ float4 red[4][ROWS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
+    const bool live = col < N;
     const uint64_t k_begin = static_cast<uint64_t>(blockIdx.y) * k_per_slice;
     const uint64_t k_end = min(K, k_begin + k_per_slice);
     float4 acc[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (col < N) {
-        constexpr int kU = 4;
+    if (live) {
+        constexpr int kU = 8;
         uint64_t kk = k_begin + wave;
         for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
             float4 bv[kU];
@@ -300,40 +304,87 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
             }
         }
     }
-    if (wave > 0) {
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) red[wave - 1][r][lane] = acc[r];
-    }
+    for (int r = 0; r < ROWS; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    if (wave == 0 && col < N) {
+    if (wave != 0 || !live) return;
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            float4 v = acc[r];
+    for (int r = 0; r < ROWS; ++r) {
+        float4 v = red[0][r][lane];
 #pragma unroll
-            for (int w = 0; w < 3; ++w) {
-                const float4 o = red[w][r][lane];
-                v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+        for (int w = 1; w < 4; ++w) {
+            const float4 o = red[w][r][lane];
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+        }
+        if (slices == 1) {
+            if (addend_mode == 1) {
+                const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
+                v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+            } else if (addend_mode == 2) {
+                const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + col);
+                v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
             }
+            *reinterpret_cast<float4*>(C + r * N + col) = v;
+        } else {
             *reinterpret_cast<float4*>(partial + (static_cast<uint64_t>(blockIdx.y) * ROWS + r) * N + col) = v;
         }
     }
 }
 
-// out[row][col] = sum over slices in order (+ addend).
+// C = the slices' partial sums (+ addend). A workgroup covers 256 columns:
+// wave w adds a fixed quarter of the slices (eight loads in flight), then
+// the quarters are added in order -- the same order on every run.
 template <int ROWS>
-__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partial,
-                                                          float* __restrict__ C, uint64_t M,
-                                                          uint64_t N, uint64_t slices,
-                                                          const float* __restrict__ addend,
-                                                          int addend_mode) {
-    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= M * N) return;
-    const uint64_t row = idx / N, col = idx % N;
-    float v = 0.0f;
-    for (uint64_t s = 0; s < slices; ++s) v += partial[(s * ROWS + row) * N + col];
-    if (addend_mode == 1) v = v + addend[col];
-    else if (addend_mode == 2) v = v + addend[row * N + col];
-    C[idx] = v;
+__global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
+    const float* __restrict__ partial, float* __restrict__ C, uint64_t N, uint32_t slices,
+    const float* __restrict__ addend, int addend_mode) {
+    __shared__ float4 red[4][ROWS][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
+    const bool live = col < N;
+    const uint32_t quarter = (slices + 3) / 4;
+    const uint32_t s_begin = min(slices, wave * quarter), s_end = min(slices, s_begin + quarter);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) {
+            uint32_t s = s_begin;
+            for (; s + 7 < s_end; s += 8) {
+                float4 p[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    p[u] = *reinterpret_cast<const float4*>(partial + ((s + u) * static_cast<uint64_t>(ROWS) + r) * N + col);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    v.x += p[u].x; v.y += p[u].y; v.z += p[u].z; v.w += p[u].w;
+                }
+            }
+            for (; s < s_end; ++s) {
+                const float4 p = *reinterpret_cast<const float4*>(partial + (s * static_cast<uint64_t>(ROWS) + r) * N + col);
+                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+            }
+        }
+        red[wave][r][lane] = v;
+    }
+    __syncthreads();
+    if (wave != 0 || !live) return;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        float4 v = red[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 o = red[w][r][lane];
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+        }
+        if (addend_mode == 1) {
+            const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
+            v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+        } else if (addend_mode == 2) {
+            const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + col);
+            v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+        }
+        *reinterpret_cast<float4*>(C + r * N + col) = v;
+    }
 }
 
 mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
@@ -356,25 +407,32 @@ template <int ROWS>
 mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t k,
                         uint64_t n, const float* addend, int mode) {
     const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
-    // Enough k slices for ~16 waves per CU; each slice a multiple of 16 rows.
+    // About four workgroups per CU, each slice a multiple of 32 rows (four
+    // waves x eight rows in flight); one slice when the column groups alone
+    // fill the device.
     const uint64_t target_blocks = static_cast<uint64_t>(ctx->compute_units ? ctx->compute_units : 256) * 4;
     uint64_t slices = (target_blocks + col_groups - 1) / col_groups;
-    uint64_t k_per_slice = ((k + slices - 1) / slices + 15) / 16 * 16;
-    if (k_per_slice < 16) k_per_slice = 16;
+    uint64_t k_per_slice = ((k + slices - 1) / slices + 31) / 32 * 32;
+    if (k_per_slice < 32) k_per_slice = 32;
     slices = (k + k_per_slice - 1) / k_per_slice;
-    if (slices == 0) slices = 1;
+    if (slices <= 1) {
+        slices = 1;
+        k_per_slice = k;
+    }
     float* partial = nullptr;
-    mhip_status st = workspace(ctx, slices * ROWS * n * sizeof(float), &partial);
-    if (st != MHIP_OK) return st;
+    if (slices > 1) {
+        mhip_status st = workspace(ctx, slices * ROWS * n * sizeof(float), &partial);
+        if (st != MHIP_OK) return st;
+    }
     hipLaunchKernelGGL(gemv_partial_kernel<ROWS>,
                        dim3(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices)),
-                       dim3(kGemvThreads), 0, ctx->stream, a, b, partial, k, n, k_per_slice);
-    st = mhip::check_launch("matmul (decode partial sums)");
-    if (st != MHIP_OK) return st;
-    const uint64_t outs = ROWS * n;
-    hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>, dim3(static_cast<unsigned>((outs + 255) / 256)),
-                       dim3(256), 0, ctx->stream, partial, c, static_cast<uint64_t>(ROWS), n,
-                       slices, addend, mode);
+                       dim3(kGemvThreads), 0, ctx->stream, a, b, partial, c, k, n, k_per_slice,
+                       static_cast<uint32_t>(slices), addend, mode);
+    mhip_status st = mhip::check_launch("matmul (decode partial sums)");
+    if (st != MHIP_OK || slices == 1) return st;
+    hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>, dim3(static_cast<unsigned>(col_groups)),
+                       dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
+                       static_cast<uint32_t>(slices), addend, mode);
     return mhip::check_launch("matmul (decode reduction)");
 }
 

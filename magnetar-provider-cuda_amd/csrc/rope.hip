@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void rope_interleaved_vec_kernel(RopeArgs
             rotate(v.z, v.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
             v = r;
         }
-        o4[c] = v;
+        mhip::store_nt(o4 + c, v);
     }
 }
 
@@ -169,11 +169,11 @@ __global__ __launch_bounds__(kThreads) void rope_half_split_vec_kernel(RopeArgs 
             rotate(u.y, w.y, cs[p + 1], sn[p + 1], &ru.y, &rw.y);
             rotate(u.z, w.z, cs[p + 2], sn[p + 2], &ru.z, &rw.z);
             rotate(u.w, w.w, cs[p + 3], sn[p + 3], &ru.w, &rw.w);
-            o4[base + k] = ru;
-            o4[base + k + half4] = rw;
+            mhip::store_nt(o4 + base + k, ru);
+            mhip::store_nt(o4 + base + k + half4, rw);
         } else {
             const uint64_t s = base + dim4 + (k - half4);
-            o4[s] = x4[s];
+            mhip::store_nt(o4 + s, x4[s]);
         }
     }
 }

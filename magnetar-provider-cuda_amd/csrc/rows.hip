@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
             } else {
                 y = make_float4(x[v].x * inv, x[v].y * inv, x[v].z * inv, x[v].w * inv);
             }
-            o4[c] = y;
+            mhip::store_nt(o4 + c, y);
         }
     }
 }
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void softmax_vec_kernel(const float* __re
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        if (c < cols4) o4[c] = make_float4(x[v].x / s, x[v].y / s, x[v].z / s, x[v].w / s);
+        if (c < cols4) mhip::store_nt(o4 + c, make_float4(x[v].x / s, x[v].y / s, x[v].z / s, x[v].w / s));
     }
 }
 

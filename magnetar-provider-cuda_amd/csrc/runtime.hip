@@ -93,6 +93,7 @@ mhip_status mhip_ctx_create(int ordinal, mhip_ctx** out) {
     if ((err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
         (err = hipMalloc(reinterpret_cast<void**>(&ctx->flags), 256)) != hipSuccess ||
         (err = hipMemset(ctx->flags, 0, 256)) != hipSuccess ||
+
         (err = hipEventCreate(&ctx->timer_start)) != hipSuccess ||
         (err = hipEventCreate(&ctx->timer_stop)) != hipSuccess) {
         mhip_status st = mhip::from_hip(err, "creating the device context");
@@ -110,6 +111,7 @@ mhip_status mhip_ctx_destroy(mhip_ctx* ctx) {
     if (ctx->flags) (void)hipFree(ctx->flags);
     for (auto& table : ctx->rope_tables) (void)hipFree(table.device);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+
     if (ctx->timer_start) (void)hipEventDestroy(ctx->timer_start);
     if (ctx->timer_stop) (void)hipEventDestroy(ctx->timer_stop);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
