@@ -47,6 +47,16 @@ __device__ __forceinline__ void store_nt(uint4* p, uint4 v) {
     __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
 }
 
+// Streaming inputs read exactly once: a non-temporal dwordx4 load.
+__device__ __forceinline__ float4 load_nt(const float4* p) {
+    const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint4 load_nt(const uint4* p) {
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 // Records `detail` as this thread's last error and returns `status`.
 mhip_status fail(mhip_status status, const std::string& detail);
 // Maps a HIP runtime error onto the stable categories (src/error.rs:71-91).

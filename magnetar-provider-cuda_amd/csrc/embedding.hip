@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kThreads) void embedding_vec_kernel(
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             uint64_t c = c0 + static_cast<uint64_t>(u) * TPR;
-            if (c < dim4) v[u] = src[c];
+            if (c < dim4) v[u] = mhip::load_nt(src + c);
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {

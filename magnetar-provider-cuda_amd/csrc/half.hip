@@ -12,14 +12,13 @@
 //  - f16 encode uses v_cvt_f16_f32 (round-to-nearest-even, overflow to inf,
 //    subnormal results rounded) and applies the reference's NaN payload rule;
 //  - bf16 is the reference's integer rounding itself (bits + 0x7FFF + lsb).
-// Each thread moves 8 halves per 16-byte access; outputs use non-temporal
-// stores.
+// Each thread moves 8 halves per 16-byte access, non-temporal in and out.
 #include "common.hpp"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 2;
+constexpr int kUnroll = 1;
 constexpr uint64_t kPerBlock = static_cast<uint64_t>(kThreads) * kUnroll;  // 8-half slots
 
 __device__ __forceinline__ float f16_decode(uint32_t h) {
@@ -99,8 +98,8 @@ __global__ __launch_bounds__(kThreads) void half_binary_kernel(const uint16_t* _
     for (int u = 0; u < kUnroll; ++u) {
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
         if (i < full) {
-            va[u] = a4[i];
-            vb[u] = b4[i];
+            va[u] = mhip::load_nt(a4 + i);
+            vb[u] = mhip::load_nt(b4 + i);
         }
     }
 #pragma unroll

@@ -279,7 +279,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
             float4 bv[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u)
-                bv[u] = *reinterpret_cast<const float4*>(B + (kk + 4 * u) * N + col);
+                bv[u] = mhip::load_nt(reinterpret_cast<const float4*>(B + (kk + 4 * u) * N + col));
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
 #pragma unroll
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
             }
         }
         for (; kk < k_end; kk += 4) {
-            const float4 bv = *reinterpret_cast<const float4*>(B + kk * N + col);
+            const float4 bv = mhip::load_nt(reinterpret_cast<const float4*>(B + kk * N + col));
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const float a = A[r * K + kk];

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void rope_interleaved_vec_kernel(RopeArgs
     float4* o4 = reinterpret_cast<float4*>(a.out) + row * cols4;
     for (uint64_t c = threadIdx.x; c < cols4; c += kThreads) {
         const uint64_t j = (c % hw4) * 4;
-        float4 v = x4[c];
+        float4 v = mhip::load_nt(x4 + c);
         if (j < a.dimension) {
             const uint64_t p = j / 2;
             float4 r;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void rope_half_split_vec_kernel(RopeArgs 
         const uint64_t h = t / per_head, k = t % per_head;
         const uint64_t base = h * hw4;
         if (k < half4) {
-            float4 u = x4[base + k], w = x4[base + k + half4];
+            float4 u = mhip::load_nt(x4 + base + k), w = mhip::load_nt(x4 + base + k + half4);
             const uint64_t p = k * 4;
             float4 ru, rw;
             rotate(u.x, w.x, cs[p], sn[p], &ru.x, &rw.x);

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        x[v] = (live && c < cols4) ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[v] = (live && c < cols4) ? mhip::load_nt(x4 + c) : make_float4(0.f, 0.f, 0.f, 0.f);
         ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
     }
     ss = group_reduce<G>(ss, SumOp{}, scratch);
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void softmax_vec_kernel(const float* __re
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        x[v] = (live && c < cols4) ? x4[c]
+        x[v] = (live && c < cols4) ? mhip::load_nt(x4 + c)
                                    : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
         m = fmaxf(m, fmaxf(fmaxf(x[v].x, x[v].y), fmaxf(x[v].z, x[v].w)));
     }
