@@ -24,11 +24,12 @@
 //    output rescaled, so it is always a convex combination of V rows and
 //    never overflows (the reference's 1e38 known answer,
 //    src/tests_conformance.rs:2215-2312).
-//  - decode (one query row, any head dim that is a multiple of 4 up to 256):
-//    split-KV. A workgroup takes one (batch, KV head, key chunk) and all the
-//    query heads that share that KV head, streams K and V once with dwordx4
-//    loads, and writes the chunk's normalised output, max and weight sum; a
-//    second kernel merges chunks in chunk order (deterministic).
+//  - decode (one query row, head dim 4, 8, 16, ..., 256): split-KV. A
+//    workgroup takes one (batch, KV head, key chunk) and all the query heads
+//    that share that KV head, issues every K and V load of the chunk at once
+//    (non-temporal dwordx4), keeps scores and probabilities in registers, and
+//    writes the chunk's normalised output, max and weight sum; a second
+//    kernel merges the chunks in a fixed order (deterministic).
 //  - a generic kernel (any other shape): one wave per (query, head), online
 //    softmax over 64-key chunks.
 #include "common.hpp"
@@ -291,163 +292,227 @@ mhip_status launch_prefill(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
 
 constexpr int kMaxGroup = 8;
 
-// Partial record per (batch, head, chunk): [0..vd) normalised output, then max, sum.
-template <int D4>  // D / 4: lanes per key row
-__global__ __launch_bounds__(256) void attn_decode_partial_kernel(AttnArgs a, uint64_t chunk,
-                                                                  uint64_t chunks,
-                                                                  float* __restrict__ part) {
-    constexpr int kLPK = D4;            // lanes per key
-    constexpr int kKPS = 64 / kLPK;     // keys per wave step
-    constexpr int D = 4 * D4;
-    extern __shared__ float lds[];      // q [G][D], scores [G][chunk], red [4*kKPS][G][D]
-    const uint64_t group = a.heads / a.kv_heads;
-    const uint64_t c_idx = blockIdx.x % chunks;
-    const uint64_t bkv = blockIdx.x / chunks;
-    const uint64_t kvh = bkv % a.kv_heads, b = bkv / a.kv_heads;
-    const uint64_t k_begin = c_idx * chunk;
-    const uint64_t k_end = min(a.kv_seq, k_begin + chunk);
-    const uint64_t qpos = a.offset;  // the one query row: seq == 1
-    uint64_t lo, hi;
-    key_range(a, qpos, &lo, &hi);
-    const uint64_t c_lo = max(lo, k_begin), c_hi = min(hi, k_end);
-    const int n = c_lo < c_hi ? static_cast<int>(c_hi - c_lo) : 0;
+// Keys per chunk for head dim 4*D4: kDecodeSteps(D4) steps of 256/D4 keys
+// (D4 lanes hold one key row, 64/D4 keys per wave, four waves). At D >= 16
+// a chunk is 32 KB of K plus 32 KB of V.
+__host__ __device__ constexpr int decode_steps(int d4) { return d4 >= 4 ? 8 : 2 * d4; }
+__host__ __device__ constexpr int decode_chunk(int d4) { return decode_steps(d4) * 256 / d4; }
 
-    float* sq = lds;                                   // [group][D]
-    float* ss = lds + group * D;                       // [group][chunk]
-    float* sred = ss + group * chunk;                  // [4*kKPS][group][D]
-    const float* Qb = a.q + b * a.q_bs;
-    for (uint64_t i = threadIdx.x; i < group * D; i += 256) {
-        const uint64_t g = i / D, t = i % D;
-        sq[i] = Qb[(kvh * group + g) * D + t] * a.qscale;
-    }
-    __syncthreads();
+// One workgroup per (batch, KV head, key chunk). Every thread issues all of
+// its K and V loads before any arithmetic (2 * kSteps dwordx4 in flight);
+// scores, the chunk max and the probabilities stay in registers, and only
+// the per-wave partial sums meet in LDS. Writes, per query head of the
+// group, the chunk's output normalised by its own weight sum, plus the
+// chunk max (log2 domain) and weight sum.
+template <int D4, int GT>
+__global__ __launch_bounds__(256) void attn_decode_partial_kernel(
+    AttnArgs a, uint64_t key_lo, uint64_t key_hi, uint64_t chunks, float* __restrict__ part_o,
+    float* __restrict__ part_ml) {
+    constexpr int kLPK = D4;              // lanes per key
+    constexpr int kKPS = 64 / kLPK;       // keys per wave step
+    constexpr int kKPW = 4 * kKPS;        // keys per workgroup step
+    constexpr int kSteps = decode_steps(D4);
+    constexpr int D = 4 * D4;
+    __shared__ float4 sq[GT][D4];
+    __shared__ float4 red[4][GT][D4];
+    __shared__ float wm[4][GT], wl[4][GT];
+
+    // (batch, KV head) varies fastest: workgroups in flight together read
+    // whole K/V rows (all heads of the same keys) rather than one head's
+    // 4*D-byte slice of many rows.
+    const int group = static_cast<int>(a.heads / a.kv_heads);
+    const uint64_t units = gridDim.x / chunks;
+    const uint64_t c_idx = blockIdx.x / units;
+    const uint64_t bkv = blockIdx.x % units;
+    const uint64_t kvh = bkv % a.kv_heads, b = bkv / a.kv_heads;
+    const uint64_t c_lo = key_lo + c_idx * static_cast<uint64_t>(kSteps * kKPW);
+    const int n = c_lo < key_hi ? static_cast<int>(min<uint64_t>(key_hi - c_lo, kSteps * kKPW)) : 0;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / kLPK, sl = lane % kLPK;
-    const float* K = a.k + b * a.k_bs + kvh * D;
-    const float* V = a.v + b * a.v_bs + kvh * D;
     const uint64_t k_ld = a.kv_heads * D;
+    const float* K = a.k + b * a.k_bs + kvh * D + 4 * sl;
+    const float* V = a.v + b * a.v_bs + kvh * D + 4 * sl;
 
-    // Scores: key j of the chunk handled by (wave, sub) = j % (4*kKPS).
-    for (int j0 = 0; j0 < n; j0 += 4 * kKPS) {
-        const int j = j0 + wave * kKPS + sub;
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j < n) kv = *reinterpret_cast<const float4*>(K + (c_lo + j) * k_ld + 4 * sl);
-        for (uint64_t g = 0; g < group; ++g) {
-            const float4 qv = *reinterpret_cast<const float4*>(sq + g * D + 4 * sl);
-            float dot = kv.x * qv.x + kv.y * qv.y + kv.z * qv.z + kv.w * qv.w;
+    float4 kr[kSteps], vr[kSteps];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+        const int j = u * kKPW + wave * kKPS + sub;
+        kr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        vr[u] = kr[u];
+        if (j < n) {
+            kr[u] = mhip::load_nt(reinterpret_cast<const float4*>(K + (c_lo + j) * k_ld));
+            vr[u] = mhip::load_nt(reinterpret_cast<const float4*>(V + (c_lo + j) * k_ld));
+        }
+    }
+    const float* Qb = a.q + b * a.q_bs + kvh * static_cast<uint64_t>(group) * D;
+    for (int i = threadIdx.x; i < group * D4; i += 256) {
+        float4 q4 = *reinterpret_cast<const float4*>(Qb + 4 * static_cast<uint64_t>(i));
+        q4.x *= a.qscale; q4.y *= a.qscale; q4.z *= a.qscale; q4.w *= a.qscale;
+        sq[i / D4][i % D4] = q4;
+    }
+    __syncthreads();
+
+    // Scores (log2 domain) and the chunk max per head.
+    float s[GT][kSteps];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        if (g >= group) break;
+        const float4 q4 = sq[g][sl];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            float dot = kr[u].x * q4.x + kr[u].y * q4.y + kr[u].z * q4.z + kr[u].w * q4.w;
 #pragma unroll
             for (int off = kLPK / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
-            if (sl == 0 && j < n) ss[g * chunk + j] = dot;
+            const int j = u * kKPW + wave * kKPS + sub;
+            s[g][u] = j < n ? dot : -INFINITY;
+            mx = fmaxf(mx, s[g][u]);
         }
+#pragma unroll
+        for (int off = kLPK; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (lane == 0) wm[wave][g] = mx;
     }
     __syncthreads();
-    // Per head: max and weight sum over the chunk (one wave per head).
-    __shared__ float stat_m[kMaxGroup], stat_l[kMaxGroup];
-    for (uint64_t g = wave; g < group; g += 4) {
-        float mx = -INFINITY;
-        for (int j = lane; j < n; j += 64) mx = fmaxf(mx, ss[g * chunk + j]);
+
+    // Probabilities and the chunk's weight sum per head.
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        float sum = 0.0f;
-        for (int j = lane; j < n; j += 64) {
-            const float p = exp2f(ss[g * chunk + j] - mx);
-            ss[g * chunk + j] = p;
-            sum += p;
+    for (int g = 0; g < GT; ++g) {
+        if (g >= group) break;
+        const float m = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+        float l = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            s[g][u] = m == -INFINITY ? 0.0f : exp2f(s[g][u] - m);
+            l += s[g][u];
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        for (int j = lane; j < n; j += 64) ss[g * chunk + j] *= inv;
-        if (lane == 0) {
-            stat_m[g] = mx;
-            stat_l[g] = sum;
-        }
+        for (int off = kLPK; off < 64; off <<= 1) l += __shfl_xor(l, off, 64);
+        if (lane == 0) wl[wave][g] = l;
     }
     __syncthreads();
-    // Weighted mean of V rows: lane sl owns columns [4sl, 4sl+4).
-    float4 acc[kMaxGroup];
+
+    // Weighted V rows with normalised probabilities: every partial sum is a
+    // convex combination of V rows, so none overflows.
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j0 = 0; j0 < n; j0 += 4 * kKPS) {
-        const int j = j0 + wave * kKPS + sub;
-        if (j < n) {
-            const float4 vv = *reinterpret_cast<const float4*>(V + (c_lo + j) * k_ld + 4 * sl);
+    for (int g = 0; g < GT; ++g) {
+        if (g >= group) break;
+        const float l = (wl[0][g] + wl[1][g]) + (wl[2][g] + wl[3][g]);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g < static_cast<int>(group)) {
-                    const float p = ss[g * chunk + j];
-                    acc[g].x += p * vv.x;
-                    acc[g].y += p * vv.y;
-                    acc[g].z += p * vv.z;
-                    acc[g].w += p * vv.w;
-                }
-            }
+        for (int u = 0; u < kSteps; ++u) {
+            const float p = s[g][u] * inv;
+            acc.x += p * vr[u].x;
+            acc.y += p * vr[u].y;
+            acc.z += p * vr[u].z;
+            acc.w += p * vr[u].w;
         }
-    }
-    const int slot = wave * kKPS + sub;
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-        if (g < static_cast<int>(group))
-            *reinterpret_cast<float4*>(sred + (slot * group + g) * D + 4 * sl) = acc[g];
+        for (int off = kLPK; off < 64; off <<= 1) {
+            acc.x += __shfl_xor(acc.x, off, 64);
+            acc.y += __shfl_xor(acc.y, off, 64);
+            acc.z += __shfl_xor(acc.z, off, 64);
+            acc.w += __shfl_xor(acc.w, off, 64);
+        }
+        if (sub == 0) red[wave][g][sl] = acc;
+    }
     __syncthreads();
-    const uint64_t rec = D + 2;
-    for (uint64_t i = threadIdx.x; i < group * D; i += 256) {
-        const uint64_t g = i / D, t = i % D;
-        float v = 0.0f;
-        for (int s2 = 0; s2 < 4 * kKPS; ++s2) v += sred[(s2 * group + g) * D + t];
-        float* dst = part + (((b * a.heads) + kvh * group + g) * chunks + c_idx) * rec;
-        dst[t] = v;
+
+    const uint64_t bh0 = b * a.heads + kvh * static_cast<uint64_t>(group);
+    for (int i = threadIdx.x; i < group * D4; i += 256) {
+        const int g = i / D4, t = i % D4;
+        float4 o = red[0][g][t];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 r = red[w][g][t];
+            o.x += r.x; o.y += r.y; o.z += r.z; o.w += r.w;
+        }
+        const float l = (wl[0][g] + wl[1][g]) + (wl[2][g] + wl[3][g]);
+        const uint64_t rec = (bh0 + g) * chunks + c_idx;
+        *reinterpret_cast<float4*>(part_o + rec * D + 4 * t) = o;
         if (t == 0) {
-            dst[D] = stat_m[g];
-            dst[D + 1] = stat_l[g];
+            const float m = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+            *reinterpret_cast<float2*>(part_ml + 2 * rec) = make_float2(m, l);
         }
     }
 }
 
-// Merges the chunk records of one (batch, head) in chunk order.
-__global__ __launch_bounds__(256) void attn_decode_combine_kernel(AttnArgs a, uint64_t chunks,
-                                                                  const float* __restrict__ part) {
+// Merges the chunk records of one (batch, head): out = sum_c w_c o_c with
+// w_c = l_c 2^(m_c - M) / sum_c' l_c' 2^(m_c' - M). Thread groups of D4
+// lanes take chunks round-robin; the groups' sums meet in LDS in a fixed
+// order, so every run adds in the same order.
+template <int D4>
+__global__ __launch_bounds__(256) void attn_decode_combine_kernel(
+    AttnArgs a, uint64_t chunks, const float* __restrict__ part_o,
+    const float* __restrict__ part_ml) {
+    constexpr int D = 4 * D4;
+    constexpr int kGroups = 256 / D4;
+    __shared__ float rm[4], rt[4];
+    __shared__ float4 red[kGroups][D4];
     const uint64_t bh = blockIdx.x;
     const uint64_t head = bh % a.heads, b = bh / a.heads;
-    const uint64_t D = a.vd, rec = D + 2;
-    const float* p = part + bh * chunks * rec;
+    const float* ml = part_ml + 2 * bh * chunks;
+    const float* po = part_o + bh * chunks * D;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
     float mx = -INFINITY;
-    for (uint64_t c = 0; c < chunks; ++c) mx = fmaxf(mx, p[c * rec + D]);
-    float total = 0.0f;
-    if (mx != -INFINITY)
-        for (uint64_t c = 0; c < chunks; ++c) total += p[c * rec + D + 1] * exp2f(p[c * rec + D] - mx);
-    float* orow = a.out + b * a.o_bs + head * D;
-    for (uint64_t t = threadIdx.x; t < D; t += 256) {
-        float v = 0.0f;
-        if (total > 0.0f) {
-            for (uint64_t c = 0; c < chunks; ++c) {
-                const float w = p[c * rec + D + 1] * exp2f(p[c * rec + D] - mx) / total;
-                if (w > 0.0f) v += w * p[c * rec + t];
+    for (uint64_t c = threadIdx.x; c < chunks; c += 256) mx = fmaxf(mx, ml[2 * c]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) rm[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3]));
+    float tot = 0.0f;
+    if (M != -INFINITY)
+        for (uint64_t c = threadIdx.x; c < chunks; c += 256) {
+            const float2 e = *reinterpret_cast<const float2*>(ml + 2 * c);
+            if (e.y > 0.0f) tot += e.y * exp2f(e.x - M);
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
+    if (lane == 0) rt[wave] = tot;
+    __syncthreads();
+    const float total = (rt[0] + rt[1]) + (rt[2] + rt[3]);
+
+    const int gi = threadIdx.x / D4, t = threadIdx.x % D4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (total > 0.0f) {
+        const float inv_total = 1.0f / total;
+        uint64_t c = gi;
+        for (; c + 3 * kGroups < chunks; c += 4 * kGroups) {
+            float4 o[4];
+            float2 e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                o[u] = *reinterpret_cast<const float4*>(po + (c + u * kGroups) * D + 4 * t);
+                e[u] = *reinterpret_cast<const float2*>(ml + 2 * (c + u * kGroups));
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float w = e[u].y > 0.0f ? e[u].y * exp2f(e[u].x - M) * inv_total : 0.0f;
+                acc.x += w * o[u].x; acc.y += w * o[u].y; acc.z += w * o[u].z; acc.w += w * o[u].w;
             }
         }
-        orow[t] = v;
+        for (; c < chunks; c += kGroups) {
+            const float4 o = *reinterpret_cast<const float4*>(po + c * D + 4 * t);
+            const float2 e = *reinterpret_cast<const float2*>(ml + 2 * c);
+            const float w = e.y > 0.0f ? e.y * exp2f(e.x - M) * inv_total : 0.0f;
+            acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
+        }
     }
+    red[gi][t] = acc;
+    __syncthreads();
+    if (threadIdx.x >= D4) return;
+    float4 v = red[0][t];
+    for (int g = 1; g < kGroups; ++g) {
+        const float4 r = red[g][t];
+        v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w;
+    }
+    *reinterpret_cast<float4*>(a.out + b * a.o_bs + head * D + 4 * t) = v;
 }
 
-template <int D4>
-mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
-    constexpr int D = 4 * D4;
-    const uint64_t group = a.heads / a.kv_heads;
-    const uint64_t units = batch * a.kv_heads;
-    const uint64_t target = static_cast<uint64_t>(ctx->compute_units ? ctx->compute_units : 256) * 4;
-    uint64_t chunks = (target + units - 1) / units;
-    uint64_t chunk = (a.kv_seq + chunks - 1) / chunks;
-    chunk = (chunk + 63) / 64 * 64;
-    if (chunk < 64) chunk = 64;
-    // Keep scores + reduction scratch within 64 KiB of LDS.
-    const uint64_t red = static_cast<uint64_t>(4 * (64 / D4)) * group * D;
-    while (chunk > 64 && (group * D + group * chunk + red) * 4 > 65536) chunk -= 64;
-    if ((group * D + group * chunk + red) * 4 > 65536) return MHIP_CAPTURE_UNSUPPORTED;  // caller falls back
-    chunks = (a.kv_seq + chunk - 1) / chunk;
-    if (chunks == 0) chunks = 1;
-    const uint64_t rec = D + 2;
-    const size_t bytes = batch * a.heads * chunks * rec * sizeof(float);
+mhip_status attention_workspace(mhip_ctx* ctx, size_t bytes, float** out) {
     if (ctx->workspace_bytes < bytes) {
         if (ctx->workspace) {
             (void)hipStreamSynchronize(ctx->stream);
@@ -459,15 +524,57 @@ mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
         if (err != hipSuccess) return mhip::from_hip(err, "allocating the attention workspace");
         ctx->workspace_bytes = bytes;
     }
-    float* part = static_cast<float*>(ctx->workspace);
-    const size_t lds = (group * D + group * chunk + red) * sizeof(float);
-    hipLaunchKernelGGL(attn_decode_partial_kernel<D4>, dim3(static_cast<unsigned>(units * chunks)),
-                       dim3(256), lds, ctx->stream, a, chunk, chunks, part);
-    mhip_status st = mhip::check_launch("attention (decode chunks)");
+    *out = static_cast<float*>(ctx->workspace);
+    return MHIP_OK;
+}
+
+template <int D4, int GT>
+mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
+    constexpr int D = 4 * D4;
+    constexpr uint64_t kChunk = decode_chunk(D4);
+    // The one query (seq == 1) sits at position kv_seq - 1 in every batch
+    // row and head, so the admitted key range is the same for all of them.
+    uint64_t lo, hi;
+    {
+        uint64_t upper = a.causal ? a.offset + 1 : a.kv_seq;
+        if (upper > a.kv_seq) upper = a.kv_seq;
+        uint64_t lower = 0;
+        if (a.window >= 0) {
+            const uint64_t w = static_cast<uint64_t>(a.window);
+            const uint64_t back = w > 0 ? w - 1 : 0;
+            lower = a.offset > back ? a.offset - back : 0;
+            if (lower > upper) lower = upper;
+        }
+        lo = lower;
+        hi = upper;
+    }
+    uint64_t chunks = (hi - lo + kChunk - 1) / kChunk;
+    if (chunks == 0) chunks = 1;
+    const uint64_t units = batch * a.kv_heads;
+    if (units * chunks >= (1ULL << 31))
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention decode: too many key chunks");
+    const uint64_t records = batch * a.heads * chunks;
+    float* part = nullptr;
+    mhip_status st = attention_workspace(ctx, records * (D + 2) * sizeof(float), &part);
     if (st != MHIP_OK) return st;
-    hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(static_cast<unsigned>(batch * a.heads)),
-                       dim3(256), 0, ctx->stream, a, chunks, part);
+    float* part_o = part;
+    float* part_ml = part + records * D;
+    hipLaunchKernelGGL((attn_decode_partial_kernel<D4, GT>), dim3(static_cast<unsigned>(units * chunks)),
+                       dim3(256), 0, ctx->stream, a, lo, hi, chunks, part_o, part_ml);
+    st = mhip::check_launch("attention (decode chunks)");
+    if (st != MHIP_OK) return st;
+    hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
+                       dim3(256), 0, ctx->stream, a, chunks, part_o, part_ml);
     return mhip::check_launch("attention (decode combine)");
+}
+
+template <int D4>
+mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
+    const uint64_t group = a.heads / a.kv_heads;
+    if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch);
+    if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch);
+    if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch);
+    return launch_decode_group<D4, 8>(ctx, a, batch);
 }
 
 // ---------------------------------------------------------------------------
@@ -605,7 +712,7 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
             case 64: st = launch_decode<64>(ctx, a, batch); break;
             default: break;
         }
-        if (st != MHIP_CAPTURE_UNSUPPORTED) return st;  // else: no decode kernel fits
+        if (st != MHIP_CAPTURE_UNSUPPORTED) return st;  // else: no decode kernel for this d
     }
     if (aligned && vd == d && d == 128) return launch_prefill<128, 128>(ctx, a, batch);
     if (aligned && vd == d && d == 64) return launch_prefill<64, 64>(ctx, a, batch);

@@ -57,6 +57,40 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
     return make_uint4(t.x, t.y, t.z, t.w);
 }
 
+// silu(v) = v * (1 / (1 + e^-v)) (src/kernels.cu:73-79).
+__device__ __forceinline__ float silu1(float v) { return v * (1.0f / (1.0f + expf(-v))); }
+
+// An embedding id is valid iff id >= 0, id == floor(id) and id < vocab
+// (src/kernels.cu:127-176); NaN fails the first test.
+__device__ __forceinline__ bool valid_embedding_id(float raw, uint64_t vocab, uint64_t* id) {
+    if (raw < 0.0f || raw != floorf(raw)) return false;
+    if (static_cast<double>(raw) >= static_cast<double>(vocab)) return false;
+    *id = static_cast<uint64_t>(raw);
+    return true;
+}
+
+// RoPE: the position of `row` (src/kernels.cu:1190-1196), the scaled
+// (cos, sin) of pair p from a (frequency, amplitude) table of 2 * half
+// floats, and the rotation of one pair.
+__device__ __forceinline__ float rope_position(uint64_t offset, uint64_t row, float scale) {
+    return static_cast<float>(offset + row) * scale;
+}
+__device__ __forceinline__ void rope_pair_cs(float position, const float* table, uint64_t half,
+                                             uint64_t p, float* cs, float* sn) {
+    const float angle = position * table[p];
+    const float amp = table[half + p];
+    float s, c;
+    sincosf(angle, &s, &c);
+    *sn = s * amp;
+    *cs = c * amp;
+}
+__device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float* o1,
+                                            float* o2) {
+#pragma clang fp contract(off)
+    *o1 = a * c - b * s;
+    *o2 = a * s + b * c;
+}
+
 // Records `detail` as this thread's last error and returns `status`.
 mhip_status fail(mhip_status status, const std::string& detail);
 // Maps a HIP runtime error onto the stable categories (src/error.rs:71-91).
@@ -68,6 +102,11 @@ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // Checks the launch that was just enqueued.
 mhip_status check_launch(const char* what);
+
+// The device (frequency, amplitude) table of a RoPE call's pairs, computed
+// on the host with the f32 operations of src/kernels.cu:1197-1221 and cached
+// per context.
+mhip_status rope_device_table(mhip_ctx* ctx, const mhip_rope_params& p, const float** table);
 
 }  // namespace mhip
 

@@ -11,10 +11,15 @@
 // (`key_count`). Here the K and V projections are written straight into
 // their cache rows and rotated in place, so the append costs no copy, and the
 // residual adds ride in the matmul epilogues (matmul-residual, bit-identical
-// to matmul + add). All launches go on the context's stream; nothing waits.
+// to matmul + add). For decode (up to 8 rows) the Q/K/V and gate/up
+// projections each run as one fused GEMV set whose reduction applies RoPE or
+// silu * up, and the embedding row is normalised as it is gathered; every
+// fusion is bit-identical to the separate calls. All launches go on the
+// context's stream; nothing waits.
 #include <cstring>
 #include <string>
 
+#include "internal.hpp"
 #include "magnetar_hip.h"
 
 namespace {
@@ -79,18 +84,36 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
         if ((st = (call)) != MHIP_OK) \
             return st;                 \
     } while (0)
-    MHIP_TRY(mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
-    MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
-    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, 0, 0, nullptr, 0));
-    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wk, k_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
-    MHIP_TRY(mhip_matmul_f32(ctx, h, w->wv, v_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
-    mhip_rope_params rp;
-    mhip_rope_params_default(&rp, c.head_dim, c.heads);
-    rp.base = c.rope_base;
-    rp.position_offset = position;
-    MHIP_TRY(mhip_rope_f32(ctx, q, q, seq, c.heads * c.head_dim, &rp));
-    rp.head_count = c.kv_heads;
-    MHIP_TRY(mhip_rope_f32(ctx, k_rows, k_rows, seq, kv_dim, &rp));
+    // Embedding + RMSNorm in one pass where the row fits the fused kernel.
+    st = mhip::embed_rmsnorm_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, w->attn_norm,
+                                 c.eps, x, h);
+    if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        MHIP_TRY(mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
+        MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
+    } else if (st != MHIP_OK) {
+        return st;
+    }
+    mhip_rope_params rope[2];
+    mhip_rope_params_default(&rope[0], c.head_dim, c.heads);
+    rope[0].base = c.rope_base;
+    rope[0].position_offset = position;
+    rope[1] = rope[0];
+    rope[1].head_count = c.kv_heads;
+    // Decode (a few rows): Q, K, V as one set of GEMVs with RoPE applied where
+    // their split-k sums are added. Otherwise three matmuls and two RoPE calls.
+    const mhip::GemvTarget qkv[3] = {{w->wq, c.heads * c.head_dim, q},
+                                     {w->wk, kv_dim, k_rows},
+                                     {w->wv, kv_dim, v_rows}};
+    st = mhip::gemv_set_f32(ctx, h, seq, c.hidden, qkv, 3, mhip::kGemvRopeQK, rope);
+    if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, 0, 0, nullptr, 0));
+        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wk, k_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
+        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wv, v_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
+        MHIP_TRY(mhip_rope_f32(ctx, q, q, seq, c.heads * c.head_dim, &rope[0]));
+        MHIP_TRY(mhip_rope_f32(ctx, k_rows, k_rows, seq, kv_dim, &rope[1]));
+    } else if (st != MHIP_OK) {
+        return st;
+    }
     mhip_attention_params ap;
     std::memset(&ap, 0, sizeof(ap));
     ap.seq_len = seq;
@@ -106,9 +129,17 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
     MHIP_TRY(mhip_matmul_f32(ctx, a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, 0, 0, x, 2));
     MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
-    MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_gate, g, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
-    MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_up, u, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
-    MHIP_TRY(mhip_silu_mul_f32(ctx, g, u, g, seq * c.ffn));
+    // Decode: gate and up as one set of GEMVs whose reduction writes
+    // silu(gate) * up. Otherwise two matmuls and silu-mul.
+    const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};
+    st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr);
+    if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_gate, g, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
+        MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_up, u, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
+        MHIP_TRY(mhip_silu_mul_f32(ctx, g, u, g, seq * c.ffn));
+    } else if (st != MHIP_OK) {
+        return st;
+    }
     MHIP_TRY(mhip_matmul_f32(ctx, g, w->w_down, out, seq, c.ffn, c.hidden, 0, 0, x2, 2));
 #undef MHIP_TRY
     return MHIP_OK;

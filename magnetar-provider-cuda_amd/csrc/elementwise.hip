@@ -18,7 +18,7 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 1;
 constexpr uint64_t kPerBlock = static_cast<uint64_t>(kThreads) * kUnroll;  // float4 slots
 
-__device__ __forceinline__ float silu1(float v) { return v * (1.0f / (1.0f + expf(-v))); }
+using mhip::silu1;
 
 struct AddOp {
     __device__ float operator()(float a, float b) const { return a + b; }

@@ -15,12 +15,7 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ bool valid_id(float raw, uint64_t vocab, uint64_t* id) {
-    if (raw < 0.0f || raw != floorf(raw)) return false;  // negative, fractional or NaN
-    if (static_cast<double>(raw) >= static_cast<double>(vocab)) return false;
-    *id = static_cast<uint64_t>(raw);
-    return true;
-}
+using mhip::valid_embedding_id;
 
 // TPR threads per row, 256 / TPR rows per workgroup, UNROLL vectors per
 // thread in flight.
@@ -33,7 +28,7 @@ __global__ __launch_bounds__(kThreads) void embedding_vec_kernel(
     const int lane = threadIdx.x % TPR;
     if (row >= num_ids) return;
     uint64_t id = 0;
-    if (!valid_id(ids[row], vocab, &id)) {
+    if (!valid_embedding_id(ids[row], vocab, &id)) {
         if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
         return;
     }
@@ -62,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void embedding_scalar_kernel(
     const int lane = threadIdx.x % 64;
     if (row >= num_ids) return;
     uint64_t id = 0;
-    if (!valid_id(ids[row], vocab, &id)) {
+    if (!valid_embedding_id(ids[row], vocab, &id)) {
         if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
         return;
     }

@@ -1,0 +1,51 @@
+// Fused entry points used inside the library (the decoder block), not part
+// of the C ABI. Host-only declarations: includable from g++-built sources.
+//
+// Each one computes exactly what the separate ABI calls it replaces compute
+// -- same kernels' arithmetic, same split-k slicing, same summation order --
+// so a chain that uses them is bit-identical to the unfused chain; only the
+// launches (and the intermediate HBM round trips) go away.
+#pragma once
+
+#include <cstdint>
+
+#include "magnetar_hip.h"
+
+namespace mhip {
+
+// out = mhip_embedding_f32(table, ids) and h = mhip_rmsnorm_f32(out, weight,
+// eps) in one launch: the table row is read once, normalised from registers
+// and written to both. An invalid id raises MHIP_FLAG_EMBEDDING_INVALID_ID
+// and leaves that row of both outputs unwritten, as the embedding does.
+// Requires dim % 4 == 0, 16-byte aligned buffers and dim <= 16384; returns
+// MHIP_LAYOUT_UNSUPPORTED otherwise (the caller then runs the two calls).
+mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const float* table, uint64_t vocab, uint64_t dim,
+                              const float* ids, uint64_t rows, const float* weight, float eps,
+                              float* out, float* h);
+
+// One decode projection: out[rows, n] = a[rows, k] . b[k, n].
+struct GemvTarget {
+    const float* b;
+    uint64_t n;
+    float* out;
+};
+
+// Epilogues applied where the split-k partial sums are added up.
+enum GemvEpilogue : int {
+    kGemvPlain = 0,    // every target stored as is
+    kGemvRopeQK = 1,   // targets 0 and 1 rotated by `rope[0]`, `rope[1]` (Q, K); 2 plain (V)
+    kGemvSiluMul = 2,  // targets[0].out = silu(a.b0) * (a.b1); b0, b1 of equal shape
+};
+
+// Up to three projections of the same input `a` (rows <= 8) in two
+// launches: one over every target's k-slices, one that adds each target's
+// slices and applies the epilogue. Equal to mhip_matmul_f32 per target
+// followed by mhip_rope_f32 / mhip_silu_mul_f32, bit for bit. Returns
+// MHIP_LAYOUT_UNSUPPORTED when a target does not fit the decode GEMV
+// (n % 4, alignment, rows > 8) or the rope parameters are not the vector
+// interleaved form; the caller then runs the separate calls.
+mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
+                         const GemvTarget* targets, int count, int epilogue,
+                         const mhip_rope_params* rope);
+
+}  // namespace mhip

@@ -24,6 +24,7 @@
 //    workspace and a second launch adds them in a fixed order
 //    (deterministic), four waves per 256 columns.
 #include "common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -255,19 +256,20 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c,
 constexpr int kGemvThreads = 256;
 constexpr int kGemvCols = 256;  // columns per workgroup: 64 lanes x 4
 
-// Workgroup (column group x, k slice y): its 4 waves split the slice's rows
-// and meet in LDS. With one slice it writes C (+ addend) itself; otherwise it
-// writes the slice's partial sums for gemv_reduce_kernel.
+// One workgroup's share of a decode GEMV: column group `cg` (256 columns)
+// and k slice `slice`. Its 4 waves split the slice's rows and meet in LDS.
+// `direct`: write C (+ addend) itself (the only slice); otherwise write the
+// slice's partial sums for the reduction.
 template <int ROWS>
-__global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
+__device__ __forceinline__ void gemv_partial_body(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ partial,
-    float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
-    const float* __restrict__ addend, int addend_mode) {
+    float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t cg,
+    uint32_t slice, bool direct, const float* __restrict__ addend, int addend_mode) {
     __shared__ float4 red[4][ROWS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
+    const uint64_t col = static_cast<uint64_t>(cg) * kGemvCols + lane * 4;
     const bool live = col < N;
-    const uint64_t k_begin = static_cast<uint64_t>(blockIdx.y) * k_per_slice;
+    const uint64_t k_begin = static_cast<uint64_t>(slice) * k_per_slice;
     const uint64_t k_end = min(K, k_begin + k_per_slice);
     float4 acc[ROWS];
 #pragma unroll
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
             const float4 o = red[w][r][lane];
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
         }
-        if (slices == 1) {
+        if (direct) {
             if (addend_mode == 1) {
                 const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
                 v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
@@ -326,22 +328,31 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
             }
             *reinterpret_cast<float4*>(C + r * N + col) = v;
         } else {
-            *reinterpret_cast<float4*>(partial + (static_cast<uint64_t>(blockIdx.y) * ROWS + r) * N + col) = v;
+            *reinterpret_cast<float4*>(partial + (static_cast<uint64_t>(slice) * ROWS + r) * N + col) = v;
         }
     }
 }
 
-// C = the slices' partial sums (+ addend). A workgroup covers 256 columns:
-// wave w adds a fixed quarter of the slices (eight loads in flight), then
-// the quarters are added in order -- the same order on every run.
 template <int ROWS>
-__global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
-    const float* __restrict__ partial, float* __restrict__ C, uint64_t N, uint32_t slices,
+__global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ partial,
+    float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
     const float* __restrict__ addend, int addend_mode) {
+    gemv_partial_body<ROWS>(A, B, partial, C, K, N, k_per_slice, blockIdx.x, blockIdx.y,
+                            slices == 1, addend, addend_mode);
+}
+
+// Sum of the slices' partial sums of 256 columns: wave w adds a fixed
+// quarter of the slices (eight loads in flight), then wave 0 adds the
+// quarters in order -- the same order on every run. The result is valid in
+// wave 0 only; every thread of the workgroup must call it (it synchronises),
+// and a second call must come after a __syncthreads().
+template <int ROWS>
+__device__ __forceinline__ void gemv_reduce_sum(const float* __restrict__ partial, uint64_t N,
+                                                uint32_t slices, uint64_t col, bool live,
+                                                float4 (&out)[ROWS]) {
     __shared__ float4 red[4][ROWS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
-    const bool live = col < N;
     const uint32_t quarter = (slices + 3) / 4;
     const uint32_t s_begin = min(slices, wave * quarter), s_end = min(slices, s_begin + quarter);
 #pragma unroll
@@ -367,7 +378,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
         red[wave][r][lane] = v;
     }
     __syncthreads();
-    if (wave != 0 || !live) return;
+    if (wave != 0) return;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         float4 v = red[0][r][lane];
@@ -376,14 +387,133 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
             const float4 o = red[w][r][lane];
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
         }
+        out[r] = v;
+    }
+}
+
+// C = the slices' partial sums (+ addend).
+template <int ROWS>
+__global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
+    const float* __restrict__ partial, float* __restrict__ C, uint64_t N, uint32_t slices,
+    const float* __restrict__ addend, int addend_mode) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
+    const bool live = col < N;
+    float4 v[ROWS];
+    gemv_reduce_sum<ROWS>(partial, N, slices, col, live, v);
+    if (wave != 0 || !live) return;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
         if (addend_mode == 1) {
             const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
-            v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+            v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
         } else if (addend_mode == 2) {
             const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + col);
-            v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+            v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
         }
-        *reinterpret_cast<float4*>(C + r * N + col) = v;
+        *reinterpret_cast<float4*>(C + r * N + col) = v[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Sets of decode GEMVs over one input, with fused epilogues
+// ---------------------------------------------------------------------------
+
+struct GemvSeg {
+    const float* b;
+    float* partial;
+    float* out;
+    uint64_t n;
+    uint64_t k_per_slice;
+    uint32_t col_groups, slices;
+    uint32_t first_block;  // this segment's first workgroup in the partial launch
+    uint32_t first_group;  // ... and in the reduction launch
+};
+
+struct GemvSet {
+    GemvSeg seg[3];
+    int count;
+};
+
+// Rotation of one projection's rows: interleaved pairs, head_width and
+// dimension multiples of 4 (the vector RoPE kernel's case).
+struct RopeEpi {
+    const float* table;  // [half] frequencies then [half] amplitudes
+    uint64_t head_width, dimension, half, offset;
+    float scale;
+};
+
+// Segment `i` of the set with constant indices, so the fields stay in the
+// kernel argument segment.
+__device__ __forceinline__ GemvSeg pick(const GemvSet& set, int i) {
+    if (i == 0) return set.seg[0];
+    if (i == 1) return set.seg[1];
+    return set.seg[2];
+}
+
+template <int ROWS>
+__global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const float* __restrict__ A,
+                                                                        uint64_t K, GemvSet set) {
+    const uint32_t b = blockIdx.x;
+    const int i = (set.count > 2 && b >= set.seg[2].first_block) ? 2
+                  : (set.count > 1 && b >= set.seg[1].first_block) ? 1 : 0;
+    const GemvSeg s = pick(set, i);
+    const uint32_t local = b - s.first_block;
+    gemv_partial_body<ROWS>(A, s.b, s.partial, nullptr, K, s.n, s.k_per_slice,
+                            local % s.col_groups, local / s.col_groups, false, nullptr, 0);
+}
+
+__device__ __forceinline__ float4 rope_vec(const RopeEpi& e, uint64_t row, uint64_t col, float4 v) {
+    const uint64_t j = col % e.head_width;
+    if (j >= e.dimension) return v;
+    const uint64_t p = j / 2;
+    const float position = mhip::rope_position(e.offset, row, e.scale);
+    float c0, s0, c1, s1;
+    mhip::rope_pair_cs(position, e.table, e.half, p, &c0, &s0);
+    mhip::rope_pair_cs(position, e.table, e.half, p + 1, &c1, &s1);
+    float4 r;
+    mhip::rope_rotate(v.x, v.y, c0, s0, &r.x, &r.y);
+    mhip::rope_rotate(v.z, v.w, c1, s1, &r.z, &r.w);
+    return r;
+}
+
+template <int ROWS>
+__global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet set, int epilogue,
+                                                                       RopeEpi rope_q,
+                                                                       RopeEpi rope_k) {
+    const uint32_t b = blockIdx.x;
+    const int i = (set.count > 2 && b >= set.seg[2].first_group) ? 2
+                  : (set.count > 1 && b >= set.seg[1].first_group) ? 1 : 0;
+    const GemvSeg s = pick(set, i);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t col = static_cast<uint64_t>(b - s.first_group) * kGemvCols + lane * 4;
+    const bool live = col < s.n;
+    float4 v[ROWS];
+    gemv_reduce_sum<ROWS>(s.partial, s.n, s.slices, col, live, v);
+    if (epilogue == mhip::kGemvSiluMul) {
+        // Up projection: the same columns of segment 1.
+        const GemvSeg u = pick(set, 1);
+        float4 w[ROWS];
+        __syncthreads();
+        gemv_reduce_sum<ROWS>(u.partial, u.n, u.slices, col, live, w);
+        if (wave != 0 || !live) return;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            float4 o;
+            o.x = mhip::silu1(v[r].x) * w[r].x;
+            o.y = mhip::silu1(v[r].y) * w[r].y;
+            o.z = mhip::silu1(v[r].z) * w[r].z;
+            o.w = mhip::silu1(v[r].w) * w[r].w;
+            *reinterpret_cast<float4*>(s.out + r * s.n + col) = o;
+        }
+        return;
+    }
+    if (wave != 0 || !live) return;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        float4 o = v[r];
+        if (epilogue == mhip::kGemvRopeQK && i < 2) o = rope_vec(i == 0 ? rope_q : rope_k, r, col, o);
+        *reinterpret_cast<float4*>(s.out + r * s.n + col) = o;
     }
 }
 
@@ -403,13 +533,12 @@ mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
     return MHIP_OK;
 }
 
-template <int ROWS>
-mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t k,
-                        uint64_t n, const float* addend, int mode) {
+// Split-k shape of a decode GEMV: about four workgroups per CU, each slice a
+// multiple of 32 rows (four waves x eight rows in flight); one slice when
+// the column groups alone fill the device.
+void gemv_slicing(const mhip_ctx* ctx, uint64_t k, uint64_t n, uint64_t* slices_out,
+                  uint64_t* k_per_slice_out) {
     const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
-    // About four workgroups per CU, each slice a multiple of 32 rows (four
-    // waves x eight rows in flight); one slice when the column groups alone
-    // fill the device.
     const uint64_t target_blocks = static_cast<uint64_t>(ctx->compute_units ? ctx->compute_units : 256) * 4;
     uint64_t slices = (target_blocks + col_groups - 1) / col_groups;
     uint64_t k_per_slice = ((k + slices - 1) / slices + 31) / 32 * 32;
@@ -419,6 +548,16 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c,
         slices = 1;
         k_per_slice = k;
     }
+    *slices_out = slices;
+    *k_per_slice_out = k_per_slice;
+}
+
+template <int ROWS>
+mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t k,
+                        uint64_t n, const float* addend, int mode) {
+    const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
+    uint64_t slices, k_per_slice;
+    gemv_slicing(ctx, k, n, &slices, &k_per_slice);
     float* partial = nullptr;
     if (slices > 1) {
         mhip_status st = workspace(ctx, slices * ROWS * n * sizeof(float), &partial);
@@ -434,6 +573,20 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c,
                        dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
                        static_cast<uint32_t>(slices), addend, mode);
     return mhip::check_launch("matmul (decode reduction)");
+}
+
+template <int ROWS>
+mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
+                            const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups) {
+    uint32_t blocks = 0;
+    for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
+    hipLaunchKernelGGL(gemv_set_partial_kernel<ROWS>, dim3(blocks), dim3(kGemvThreads), 0,
+                       ctx->stream, a, k, set);
+    mhip_status st = mhip::check_launch("decode projections (partial sums)");
+    if (st != MHIP_OK) return st;
+    hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups), dim3(kGemvThreads), 0,
+                       ctx->stream, set, epilogue, rq, rk);
+    return mhip::check_launch("decode projections (reduction)");
 }
 
 mhip_status dispatch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t m,
@@ -492,3 +645,84 @@ extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const floa
         return launch_mfma<128, 128, 32, 64, 64, false, true>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     return launch_mfma<128, 128, 32, 64, 64, true, true>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
 }
+
+namespace mhip {
+
+mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
+                         const GemvTarget* targets, int count, int epilogue,
+                         const mhip_rope_params* rope) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (!a || !targets || count < 1 || count > 3 || rows == 0 || rows > kGemvMaxRows || k == 0)
+        return MHIP_LAYOUT_UNSUPPORTED;
+    if (epilogue == kGemvSiluMul && (count != 2 || targets[0].n != targets[1].n))
+        return MHIP_LAYOUT_UNSUPPORTED;
+    if (epilogue == kGemvRopeQK && (count < 2 || !rope)) return MHIP_LAYOUT_UNSUPPORTED;
+    GemvSet set{};
+    set.count = count;
+    uint64_t floats = 0, blocks = 0, groups = 0;
+    uint64_t offsets[3];
+    for (int i = 0; i < count; ++i) {
+        const GemvTarget& t = targets[i];
+        const bool needs_out = !(epilogue == kGemvSiluMul && i == 1);
+        if (!t.b || t.n == 0 || t.n % 4 != 0 || !aligned16(t.b) ||
+            (needs_out && (!t.out || !aligned16(t.out))))
+            return MHIP_LAYOUT_UNSUPPORTED;
+        GemvSeg& g = set.seg[i];
+        uint64_t slices, k_per_slice;
+        gemv_slicing(ctx, k, t.n, &slices, &k_per_slice);
+        g.b = t.b;
+        g.out = t.out;
+        g.n = t.n;
+        g.k_per_slice = k_per_slice;
+        g.col_groups = static_cast<uint32_t>((t.n + kGemvCols - 1) / kGemvCols);
+        g.slices = static_cast<uint32_t>(slices);
+        g.first_block = static_cast<uint32_t>(blocks);
+        g.first_group = static_cast<uint32_t>(groups);
+        offsets[i] = floats;
+        floats += (slices * rows * t.n + 63) / 64 * 64;
+        blocks += g.col_groups * slices;
+        if (!(epilogue == kGemvSiluMul && i == 1)) groups += g.col_groups;
+    }
+    if (blocks >= (1ULL << 31)) return MHIP_LAYOUT_UNSUPPORTED;
+    RopeEpi rq{}, rk{};
+    if (epilogue == kGemvRopeQK) {
+        for (int i = 0; i < 2; ++i) {
+            const mhip_rope_params& p = rope[i];
+            if (p.head_count == 0 || targets[i].n % p.head_count != 0) return MHIP_LAYOUT_UNSUPPORTED;
+            const uint64_t hw = targets[i].n / p.head_count;
+            if (p.half_split || p.dimension == 0 || p.dimension % 4 != 0 || p.dimension > hw ||
+                hw % 4 != 0 || !(p.base > 0.0f) || !std::isfinite(p.base) || !(p.scale > 0.0f) ||
+                !std::isfinite(p.scale) || (p.banded_factor > 0.0f && p.yarn_factor > 0.0f))
+                return MHIP_LAYOUT_UNSUPPORTED;
+            mhip_rope_params q = p;
+            if (q.rotated_pairs > q.dimension / 2) q.rotated_pairs = q.dimension / 2;
+            const float* table = nullptr;
+            mhip_status st = rope_device_table(ctx, q, &table);
+            if (st != MHIP_OK) return st;
+            RopeEpi& e = i == 0 ? rq : rk;
+            e.table = table;
+            e.head_width = hw;
+            e.dimension = q.dimension;
+            e.half = q.dimension / 2;
+            e.offset = q.position_offset;
+            e.scale = q.scale;
+        }
+    }
+    float* partial = nullptr;
+    mhip_status st = workspace(ctx, floats * sizeof(float), &partial);
+    if (st != MHIP_OK) return st;
+    for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
+    const uint32_t g = static_cast<uint32_t>(groups);
+    switch (rows) {
+        case 1: return launch_gemv_set<1>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 2: return launch_gemv_set<2>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 3: return launch_gemv_set<3>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 4: return launch_gemv_set<4>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 5: return launch_gemv_set<5>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 6: return launch_gemv_set<6>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 7: return launch_gemv_set<7>(ctx, a, k, set, epilogue, rq, rk, g);
+        default: return launch_gemv_set<8>(ctx, a, k, set, epilogue, rq, rk, g);
+    }
+}
+
+}  // namespace mhip

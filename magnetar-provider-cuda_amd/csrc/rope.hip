@@ -23,9 +23,6 @@
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr uint64_t kMaxHalf = 4096;  // LDS table: 2 x half floats, at most 32 KiB
-
 // The host-side frequency table: the f32 operations of src/kernels.cu:1197-1221.
 void rope_table(const mhip_rope_params& p, std::vector<float>& t) {
     const uint64_t half = p.dimension / 2;
@@ -88,6 +85,23 @@ mhip_status device_table(mhip_ctx* ctx, const std::vector<float>& table, const f
     return MHIP_OK;
 }
 
+}  // namespace
+
+namespace mhip {
+
+mhip_status rope_device_table(mhip_ctx* ctx, const mhip_rope_params& p, const float** table) {
+    std::vector<float> host;
+    rope_table(p, host);
+    return device_table(ctx, host, table);
+}
+
+}  // namespace mhip
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint64_t kMaxHalf = 4096;  // LDS table: 2 x half floats, at most 32 KiB
+
 struct RopeArgs {
     const float* in;
     float* out;
@@ -98,22 +112,12 @@ struct RopeArgs {
 
 // Fills LDS with (cos, sin) * amplitude for this row's pairs.
 __device__ __forceinline__ void row_sincos(const RopeArgs& a, uint64_t row, float* cs, float* sn) {
-    const float position = static_cast<float>(a.position_offset + row) * a.scale;
-    for (uint64_t p = threadIdx.x; p < a.half; p += kThreads) {
-        const float angle = position * a.table[p];
-        const float amp = a.table[a.half + p];
-        float s, c;
-        sincosf(angle, &s, &c);
-        sn[p] = s * amp;
-        cs[p] = c * amp;
-    }
+    const float position = mhip::rope_position(a.position_offset, row, a.scale);
+    for (uint64_t p = threadIdx.x; p < a.half; p += kThreads)
+        mhip::rope_pair_cs(position, a.table, a.half, p, &cs[p], &sn[p]);
 }
 
-__device__ __forceinline__ void rotate(float a, float b, float c, float s, float* o1, float* o2) {
-#pragma clang fp contract(off)
-    *o1 = a * c - b * s;
-    *o2 = a * s + b * c;
-}
+using mhip::rope_rotate;
 
 // Interleaved pairing, vector path: cols, head_width and dimension are
 // multiples of 4, so a dwordx4 at head offset j holds pairs j/2 and j/2+1
@@ -134,8 +138,8 @@ __global__ __launch_bounds__(kThreads) void rope_interleaved_vec_kernel(RopeArgs
         if (j < a.dimension) {
             const uint64_t p = j / 2;
             float4 r;
-            rotate(v.x, v.y, cs[p], sn[p], &r.x, &r.y);
-            rotate(v.z, v.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
+            rope_rotate(v.x, v.y, cs[p], sn[p], &r.x, &r.y);
+            rope_rotate(v.z, v.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
             v = r;
         }
         mhip::store_nt(o4 + c, v);
@@ -165,10 +169,10 @@ __global__ __launch_bounds__(kThreads) void rope_half_split_vec_kernel(RopeArgs 
             float4 u = mhip::load_nt(x4 + base + k), w = mhip::load_nt(x4 + base + k + half4);
             const uint64_t p = k * 4;
             float4 ru, rw;
-            rotate(u.x, w.x, cs[p], sn[p], &ru.x, &rw.x);
-            rotate(u.y, w.y, cs[p + 1], sn[p + 1], &ru.y, &rw.y);
-            rotate(u.z, w.z, cs[p + 2], sn[p + 2], &ru.z, &rw.z);
-            rotate(u.w, w.w, cs[p + 3], sn[p + 3], &ru.w, &rw.w);
+            rope_rotate(u.x, w.x, cs[p], sn[p], &ru.x, &rw.x);
+            rope_rotate(u.y, w.y, cs[p + 1], sn[p + 1], &ru.y, &rw.y);
+            rope_rotate(u.z, w.z, cs[p + 2], sn[p + 2], &ru.z, &rw.z);
+            rope_rotate(u.w, w.w, cs[p + 3], sn[p + 3], &ru.w, &rw.w);
             mhip::store_nt(o4 + base + k, ru);
             mhip::store_nt(o4 + base + k + half4, rw);
         } else {
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void rope_scalar_kernel(RopeArgs a, uint3
             const uint64_t first = half_split ? base + k : base + 2 * k;
             const uint64_t second = half_split ? base + k + a.half : base + 2 * k + 1;
             float r1, r2;
-            rotate(x[first], x[second], cs[k], sn[k], &r1, &r2);
+            rope_rotate(x[first], x[second], cs[k], sn[k], &r1, &r2);
             o[first] = r1;
             o[second] = r2;
         } else {
@@ -253,10 +257,8 @@ mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t r
     if (rows == 0) return MHIP_OK;
     if (!in || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rope: null buffer");
     if (rows >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "rope: too many rows");
-    std::vector<float> table;
-    rope_table(p, table);
     const float* dtable = nullptr;
-    mhip_status st = device_table(ctx, table, &dtable);
+    mhip_status st = mhip::rope_device_table(ctx, p, &dtable);
     if (st != MHIP_OK) return st;
     RopeArgs a{in, out, dtable, rows, cols, head_width, p.dimension, half, p.position_offset,
                p.scale};

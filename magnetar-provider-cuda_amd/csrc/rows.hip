@@ -13,6 +13,7 @@
 // (src/kernels.cu:1232-1260). The results here differ from the CPU oracle's
 // ascending sums only in summation order.
 #include "common.hpp"
+#include "internal.hpp"
 
 #include <cmath>
 
@@ -51,18 +52,27 @@ __device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
     return v;
 }
 
+// With `ids` set, row r of the input is row ids[r] of `in` (an embedding
+// table of `vocab` rows) and is also copied to `copy` row r: the embedding
+// lookup and the RMSNorm of its output in one pass.
 template <int G, int VPT>
 __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
     const float* __restrict__ in, const float* __restrict__ weight, float* __restrict__ out,
-    uint64_t rows, uint64_t cols, uint64_t weight_row_stride, float eps) {
+    uint64_t rows, uint64_t cols, uint64_t weight_row_stride, float eps,
+    const float* __restrict__ ids, uint64_t vocab, float* __restrict__ copy, uint32_t* flags) {
 #pragma clang fp contract(off)
     __shared__ float scratch[4];
     constexpr int kRowsPerBlock = kThreads / G;
     const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
     const int lane = threadIdx.x % G;
     const uint64_t cols4 = cols / 4;
-    const bool live = row < rows;  // G == 256 rows are always live; waves may not be
-    const float4* x4 = reinterpret_cast<const float4*>(in) + row * cols4;
+    bool live = row < rows;  // G == 256 rows are always live; waves may not be
+    uint64_t src = row;
+    if (ids && live && !mhip::valid_embedding_id(ids[row], vocab, &src)) {
+        if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
+        live = false;  // still takes part in the group reduction below
+    }
+    const float4* x4 = reinterpret_cast<const float4*>(in) + src * cols4;
     float4 x[VPT];
     float ss = 0.0f;
 #pragma unroll
@@ -75,12 +85,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
     if (!live) return;
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
+    float4* c4 = copy ? reinterpret_cast<float4*>(copy) + row * cols4 : nullptr;
     const float4* w4 = weight ? reinterpret_cast<const float4*>(weight + row * weight_row_stride)
                               : nullptr;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
         if (c < cols4) {
+            if (c4) mhip::store_nt(c4 + c, x[v]);
             float4 y;
             if (w4) {
                 float4 w = w4[c];
@@ -182,13 +194,21 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(const float* in,
 
 enum class RowKind { Rms, Softmax };
 
+// Embedding gather for the RMSNorm kernel (unused by the other kinds).
+struct Gather {
+    const float* ids = nullptr;
+    uint64_t vocab = 0;
+    float* copy = nullptr;
+};
+
 template <RowKind KIND, int G, int VPT>
 void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
-                uint64_t cols, uint64_t wstride, float eps) {
+                uint64_t cols, uint64_t wstride, float eps, const Gather& g) {
     const unsigned blocks = static_cast<unsigned>(mhip::ceil_div(rows, kThreads / G));
     if constexpr (KIND == RowKind::Rms)
         hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
-                           ctx->stream, in, weight, out, rows, cols, wstride, eps);
+                           ctx->stream, in, weight, out, rows, cols, wstride, eps, g.ids, g.vocab,
+                           g.copy, ctx->flags);
     else
         hipLaunchKernelGGL((softmax_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
                            ctx->stream, in, out, rows, cols, ctx->flags);
@@ -198,15 +218,15 @@ void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weig
 // does not fit the register-resident kernels.
 template <RowKind KIND>
 bool dispatch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
-                  uint64_t cols, uint64_t wstride, float eps) {
+                  uint64_t cols, uint64_t wstride, float eps, const Gather& g = Gather{}) {
     const uint64_t c4 = cols / 4;
-    if (c4 <= 64) launch_vec<KIND, 64, 1>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 128) launch_vec<KIND, 64, 2>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 256) launch_vec<KIND, 64, 4>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 512) launch_vec<KIND, 256, 2>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 1024) launch_vec<KIND, 256, 4>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 2048) launch_vec<KIND, 256, 8>(ctx, rows, in, weight, out, cols, wstride, eps);
-    else if (c4 <= 4096) launch_vec<KIND, 256, 16>(ctx, rows, in, weight, out, cols, wstride, eps);
+    if (c4 <= 64) launch_vec<KIND, 64, 1>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 128) launch_vec<KIND, 64, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 256) launch_vec<KIND, 64, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 512) launch_vec<KIND, 256, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 1024) launch_vec<KIND, 256, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 2048) launch_vec<KIND, 256, 8>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (c4 <= 4096) launch_vec<KIND, 256, 16>(ctx, rows, in, weight, out, cols, wstride, eps, g);
     else return false;
     return true;
 }
@@ -254,3 +274,24 @@ mhip_status mhip_softmax_rows_f32(mhip_ctx* ctx, const float* in, float* out, ui
 }
 
 }  // extern "C"
+
+namespace mhip {
+
+mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const float* table, uint64_t vocab, uint64_t dim,
+                              const float* ids, uint64_t rows, const float* weight, float eps,
+                              float* out, float* h) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (rows == 0) return MHIP_OK;
+    if (dim == 0 || dim % 4 != 0 || dim / 4 > 4096 || !(eps > 0.0f) || !table || !ids || !out ||
+        !h || !aligned16(table) || !aligned16(out) || !aligned16(h) ||
+        (weight && !aligned16(weight)) || rows >= (1ULL << 31))
+        return MHIP_LAYOUT_UNSUPPORTED;
+    Gather g;
+    g.ids = ids;
+    g.vocab = vocab;
+    g.copy = out;
+    dispatch_vec<RowKind::Rms>(ctx, rows, table, weight, h, dim, 0, eps, g);
+    return check_launch("embedding + rmsnorm");
+}
+
+}  // namespace mhip

@@ -96,3 +96,76 @@ def test_llama2_7b_block_prefill(dev, orc):
     err = max_normwise_err(got, want)
     print(f"llama2-7b prefill(64): {err:.2e}")
     assert err <= TOL
+
+
+def _rows_view(arr, first, count):
+    """Rows [first, first + count) of a 2-D device array, without a copy."""
+    from magnetar_hip.device import DeviceArray
+    cols = arr.shape[1]
+    return DeviceArray(arr.device, arr.ptr + first * cols * 4, (count, cols), arr.dtype,
+                       arr.half, owned=False)
+
+
+def unfused_block(dev, s, w, ids, position, k_cache, v_cache):
+    """The block as separate ABI calls (embedding, rmsnorm, three matmuls, two
+    RoPEs, attention, matmul-residual, rmsnorm, two matmuls, silu-mul,
+    matmul-residual), writing new K/V rows into the given caches."""
+    from magnetar_hip import ops
+    seq = ids.size
+    x = ops.embedding(dev, w["embedding"], ids)
+    h = ops.rmsnorm(dev, x, w["attn_norm"], s.eps)
+    q = ops.matmul(dev, h, w["wq"])
+    k_rows = _rows_view(k_cache, position, seq)
+    v_rows = _rows_view(v_cache, position, seq)
+    ops.matmul(dev, h, w["wk"], out=k_rows)
+    ops.matmul(dev, h, w["wv"], out=v_rows)
+    ops.rope(dev, q, ops.rope_params(s.head_dim, s.heads, base=s.rope_base,
+                                     position_offset=position), out=q)
+    ops.rope(dev, k_rows, ops.rope_params(s.head_dim, s.kv_heads, base=s.rope_base,
+                                          position_offset=position), out=k_rows)
+    p = ops.attention_params(seq, k_cache.shape[0], s.heads, s.head_dim, kv_head_count=s.kv_heads,
+                             causal=True, key_count=position + seq)
+    a = ops.attention(dev, q, k_cache, v_cache, p)
+    x2 = ops.matmul(dev, a, w["wo"], addend=x, addend_mode=2)
+    h2 = ops.rmsnorm(dev, x2, w["ffn_norm"], s.eps)
+    g = ops.matmul(dev, h2, w["w_gate"])
+    u = ops.matmul(dev, h2, w["w_up"])
+    f = ops.silu_mul(dev, g, u)
+    return ops.matmul(dev, f, w["w_down"], addend=x2, addend_mode=2)
+
+
+@pytest.mark.parametrize("seq,position", [(1, 40), (3, 20), (8, 0), (32, 0)])
+def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, position):
+    """The decode fusions (embedding + rmsnorm, Q/K/V GEMVs with RoPE in the
+    reduction, gate/up GEMVs with silu * up) change launches, not arithmetic:
+    the block output and the cache rows equal the unfused chain's bit for bit."""
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    s = Shapes(vocab=1024, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1376)
+    w = weights_for(orc, s, 500)
+    rows = 64
+    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=32)
+    kc = orc.normal(rows * 128, 501, 0.0, 0.5).reshape(rows, 128)
+    vc = orc.normal(rows * 128, 502, 0.0, 0.5).reshape(rows, 128)
+    block.k_cache = dev.upload(kc)
+    block.v_cache = dev.upload(vc)
+    k2, v2 = dev.upload(kc), dev.upload(vc)
+    ids = dev.upload(orc.token_ids(seq, 503 + seq, 1024))
+    got = block.forward(ids, position).numpy()
+    want = unfused_block(dev, s, block.w, ids, position, k2, v2).numpy()
+    dev.check_flags()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(block.k_cache.numpy().view(np.uint32), k2.numpy().view(np.uint32))
+    assert np.array_equal(block.v_cache.numpy().view(np.uint32), v2.numpy().view(np.uint32))
+
+
+def test_decode_block_rejects_an_invalid_token_id(dev, orc):
+    """The fused embedding + rmsnorm raises the embedding's invalid-id flag."""
+    import magnetar_hip
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    s = Shapes(vocab=64, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=512)
+    block = DecoderBlock(dev, s, weights_for(orc, s, 600), cache_rows=8, max_seq=2)
+    block.forward(dev.upload(np.array([3.0], np.float32)), 0)
+    dev.check_flags()
+    block.forward(dev.upload(np.array([64.0], np.float32)), 1)
+    with pytest.raises(magnetar_hip.MagnetarHipError):
+        dev.check_flags()
