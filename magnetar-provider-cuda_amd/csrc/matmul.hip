@@ -17,7 +17,10 @@
 //    transposed (scattered 4-byte writes land in distinct banks), +4 where
 //    it is copied as dwordx4. Tiles are ordered so that consecutive tiles
 //    share a block row of A and each of the 8 XCDs (own L2) gets a contiguous
-//    band of tiles.
+//    band of tiles. When there are too few tiles to fill the device (m = 512
+//    gives 128 tiles of 128 x 128 for 256 CUs), k is split over up to 8
+//    workgroups per tile; their partial tiles go to a workspace and a second
+//    launch adds them in split order (deterministic) with the addend.
 //  - m <= kGemvMaxRows (decode): the work is reading B once (HBM-bound), so
 //    each wave streams 256 columns of B with dwordx4 loads over one k slice,
 //    keeping m x 4 partial sums per lane; partial sums per k slice go to a
@@ -31,6 +34,24 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kGemvMaxRows = 8;
+
+// Grow-only scratch for split-k partial sums, kept on the context; stream
+// order makes reuse by the next call safe.
+mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
+    if (ctx->workspace_bytes < bytes) {
+        if (ctx->workspace) {
+            (void)hipStreamSynchronize(ctx->stream);
+            (void)hipFree(ctx->workspace);
+            ctx->workspace = nullptr;
+            ctx->workspace_bytes = 0;
+        }
+        hipError_t err = hipMalloc(&ctx->workspace, bytes);
+        if (err != hipSuccess) return mhip::from_hip(err, "allocating the matmul workspace");
+        ctx->workspace_bytes = bytes;
+    }
+    *out = static_cast<float*>(ctx->workspace);
+    return MHIP_OK;
+}
 
 // ---------------------------------------------------------------------------
 // MFMA tiles
@@ -129,10 +150,13 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
     *tn = in_group / rows_in_group;
 }
 
+// blockIdx.y is the k split: the workgroup sums k in [y * k_split,
+// min(K, (y + 1) * k_split)) and, with more than one split, writes that
+// partial product to C + y * M * N (no addend) for splitk_reduce_kernel.
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC>
 __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, uint64_t M,
-    uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode) {
+    uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     constexpr int T = Cfg::kThreads;
     extern __shared__ float lds[];
@@ -158,29 +182,33 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    const uint64_t k_begin = static_cast<uint64_t>(blockIdx.y) * k_split;
+    const uint64_t k_end = min(K, k_begin + k_split);  // slices past k_end are zero-filled
+    if (gridDim.y > 1) C += static_cast<uint64_t>(blockIdx.y) * M * N;
+
     float4 ra[Cfg::kAChunks], rb[Cfg::kBChunks];
     auto load = [&](uint64_t k0) {
         if constexpr (A_T)
-            load_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, VEC>(ra, A, M, k0, m0, K, M);
+            load_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, VEC>(ra, A, M, k0, m0, k_end, M);
         else
-            load_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, VEC>(ra, A, K, m0, k0, M, K);
+            load_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, VEC>(ra, A, K, m0, k0, M, k_end);
         if constexpr (B_T)
-            load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, K, n0, k0, N, K);
+            load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, K, n0, k0, N, k_end);
         else
-            load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, N, k0, n0, K, N);
+            load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, N, k0, n0, k_end, N);
     };
     auto store = [&](int buf) {
         store_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, Cfg::sA, !A_T>(ra, lds + buf * Cfg::kLdsA);
         store_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, Cfg::sB, B_T>(rb, lds_b0 + buf * Cfg::kLdsB);
     };
 
-    const uint64_t slices = (K + BK - 1) / BK;
-    load(0);
+    const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
+    load(k_begin);
     store(0);
     __syncthreads();
     for (uint64_t s = 0; s < slices; ++s) {
         const int buf = static_cast<int>(s & 1);
-        if (s + 1 < slices) load((s + 1) * BK);
+        if (s + 1 < slices) load(k_begin + (s + 1) * BK);
         const float* sa = lds + buf * Cfg::kLdsA + lk * Cfg::sA + wm * WM + lrow;
         const float* sb = lds_b0 + buf * Cfg::kLdsB + lk * Cfg::sB + wn * WN + lrow;
 #pragma unroll
@@ -212,13 +240,71 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
                 const uint64_t row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * lk + (r % 4);
                 if (row < M) {
                     float v = acc[i][j][r];
-                    if (addend_mode == 1) v = v + addend[col];
-                    else if (addend_mode == 2) v = v + addend[row * N + col];
+                    if (gridDim.y == 1) {
+                        if (addend_mode == 1) v = v + addend[col];
+                        else if (addend_mode == 2) v = v + addend[row * N + col];
+                    }
                     C[row * N + col] = v;
                 }
             }
         }
     }
+}
+
+// C = sum over splits s = 0, 1, ... of partial[s] (+ addend), added in split
+// order: deterministic. Four floats per thread; `vec`: as one dwordx4.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial,
+                                                            float* __restrict__ C, uint64_t M,
+                                                            uint64_t N, uint32_t splits,
+                                                            const float* __restrict__ addend,
+                                                            int addend_mode, int vec) {
+    const uint64_t total = M * N;
+    const uint64_t i = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= total) return;
+    if (vec && i + 3 < total) {
+        float4 v = mhip::load_nt(reinterpret_cast<const float4*>(partial + i));
+        for (uint32_t s = 1; s < splits; ++s) {
+            const float4 p = mhip::load_nt(reinterpret_cast<const float4*>(partial + s * total + i));
+            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        }
+        if (addend_mode == 1) {
+            const float4 b = *reinterpret_cast<const float4*>(addend + i % N);
+            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        } else if (addend_mode == 2) {
+            const float4 b = *reinterpret_cast<const float4*>(addend + i);
+            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        }
+        *reinterpret_cast<float4*>(C + i) = v;
+        return;
+    }
+    for (uint64_t e = i; e < i + 4 && e < total; ++e) {
+        float v = partial[e];
+        for (uint32_t s = 1; s < splits; ++s) v += partial[s * total + e];
+        if (addend_mode == 1) v = v + addend[e % N];
+        else if (addend_mode == 2) v = v + addend[e];
+        C[e] = v;
+    }
+}
+
+// How many k splits fill the device best: minimises the number of rounds of
+// `slots` resident workgroups per unit of full-k work, ceil(tiles * s /
+// slots) / s, keeping each split at least 256 deep (and a multiple of bk).
+uint64_t choose_splits(uint64_t tiles, uint64_t k, uint64_t slots, uint64_t bk,
+                       uint64_t* k_split) {
+    uint64_t best = 1;
+    double best_cost = static_cast<double>((tiles + slots - 1) / slots);
+    for (uint64_t s = 2; s <= 8; ++s) {
+        if (k / s < 256) break;
+        const double cost = static_cast<double>((tiles * s + slots - 1) / slots) / static_cast<double>(s);
+        if (cost < best_cost * (1.0 - 1e-9)) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    uint64_t per = (k + best - 1) / best;
+    per = (per + bk - 1) / bk * bk;
+    *k_split = per;
+    return (k + per - 1) / per;
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T>
@@ -227,6 +313,14 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c,
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (tiles >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: too many tiles");
+    const uint64_t slots = 2ULL * (ctx->compute_units ? ctx->compute_units : 256);
+    uint64_t k_split = k;
+    const uint64_t splits = choose_splits(tiles, k, slots, BK, &k_split);
+    float* target = c;
+    if (splits > 1) {
+        mhip_status st = workspace(ctx, splits * m * n * sizeof(float), &target);
+        if (st != MHIP_OK) return st;
+    }
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
     if (!configured) {
@@ -238,15 +332,25 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c,
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
     if (vec)
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true>),
-                           dim3(static_cast<unsigned>(tiles)), dim3(Cfg::kThreads), lds,
-                           ctx->stream, a, b, c, m, k, n, addend, mode);
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true>), grid,
+                           dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
+                           mode, k_split);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false>),
-                           dim3(static_cast<unsigned>(tiles)), dim3(Cfg::kThreads), lds,
-                           ctx->stream, a, b, c, m, k, n, addend, mode);
-    return mhip::check_launch("matmul (MFMA tiles)");
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false>), grid,
+                           dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
+                           mode, k_split);
+    mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
+    if (st != MHIP_OK || splits == 1) return st;
+    const uint64_t groups = (m * n + 1023) / 1024;
+    if (groups >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: output too large");
+    // dwordx4 path: whole rows of 4 and 16-byte aligned output and addend.
+    const int vec4 = n % 4 == 0 && mhip::aligned16(c) && (mode == 0 || mhip::aligned16(addend));
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(groups)), dim3(256), 0,
+                       ctx->stream, target, c, m, n, static_cast<uint32_t>(splits), addend, mode,
+                       vec4);
+    return mhip::check_launch("matmul (split-k reduction)");
 }
 
 // ---------------------------------------------------------------------------
@@ -517,21 +621,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
     }
 }
 
-mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
-    if (ctx->workspace_bytes < bytes) {
-        if (ctx->workspace) {
-            (void)hipStreamSynchronize(ctx->stream);
-            (void)hipFree(ctx->workspace);
-            ctx->workspace = nullptr;
-            ctx->workspace_bytes = 0;
-        }
-        hipError_t err = hipMalloc(&ctx->workspace, bytes);
-        if (err != hipSuccess) return mhip::from_hip(err, "allocating the matmul workspace");
-        ctx->workspace_bytes = bytes;
-    }
-    *out = static_cast<float*>(ctx->workspace);
-    return MHIP_OK;
-}
 
 // Split-k shape of a decode GEMV: about four workgroups per CU, each slice a
 // multiple of 32 rows (four waves x eight rows in flight); one slice when
