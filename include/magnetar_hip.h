@@ -215,6 +215,12 @@ typedef struct {
 mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
                                float* out, const mhip_attention_params* params);
 
+/* kv-write (src/kernels.rs:2270-2325): store [capacity, width] rows
+ * [row_offset, row_offset + count) = rows [count, width], in place; other rows
+ * unchanged. An overrun is ShapeUnsupported and writes nothing. */
+mhip_status mhip_kv_write_f32(mhip_ctx* ctx, float* store, uint64_t capacity, uint64_t width,
+                              const float* rows, uint64_t count, uint64_t row_offset);
+
 /* ---- decoder block, chained device-resident (src/tests_hardware_hot_path.rs:339-526) ---- */
 typedef struct {
     uint64_t hidden;            /* = heads * head_dim */
@@ -355,6 +361,16 @@ mhip_kernel_error mhip_executor_write_tensor_values(mhip_executor* ex, const cha
                                                     const float* values);
 mhip_kernel_error mhip_executor_write_zeroed_tensor(mhip_executor* ex, const char* id,
                                                     const uint64_t* shape, int rank, int dtype);
+/* KV store precisions (KvStorePrecision: F32, Tq4, Tq3). */
+typedef enum { MHIP_KV_F32 = 0, MHIP_KV_TQ4 = 1, MHIP_KV_TQ3 = 2 } mhip_kv_precision;
+/* write_zeroed_kv_store (src/executor.rs:560-602): a zeroed f32 store of
+ * `shape` under `id`, *stored = 1. The quantized TurboQuant precisions are not
+ * provided by this build: *stored = 0 and nothing is written (the caller keeps
+ * an f32 store). */
+mhip_kernel_error mhip_executor_write_zeroed_kv_store(mhip_executor* ex, const char* id,
+                                                      const uint64_t* shape, int rank,
+                                                      int precision, uint64_t head_dimension,
+                                                      int* stored);
 /* read_tensor (src/executor.rs:430-434): the stored bytes, waiting for the device. */
 mhip_kernel_error mhip_executor_read_tensor(mhip_executor* ex, const char* id, void* dst,
                                             size_t capacity, size_t* written);

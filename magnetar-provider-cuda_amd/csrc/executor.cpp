@@ -751,10 +751,68 @@ struct mhip_executor {
         raise(MHIP_KERNEL_NOT_FOUND, name);
     }
 
+    BufferPtr clone(const Buffer& b) {
+        BufferPtr copy = std::make_unique<Buffer>(ctx, b.bytes, b.shape, b.dtype);
+        check(mhip_copy(ctx, copy->ptr, b.ptr, b.bytes));
+        return copy;
+    }
+
+    // kv-write (src/executor.rs:1366-1420, src/kernels.rs:2270-2325): rows
+    // into the store's own buffer when the output is the store (a KV
+    // history), otherwise into a copy stored under the output. The store goes
+    // back under the output id either way; a failed write leaves its rows.
+    void run_kv_write(const Invocation& inv) {
+        const std::optional<uint64_t> row_offset = attr_integer(inv, "row_offset");
+        if (!row_offset) raise(MHIP_KERNEL_ATTRIBUTE_UNSUPPORTED, "row_offset");
+        if (inv.inputs.size() < 1) raise(MHIP_KERNEL_EXECUTION_FAILED, "missing input at index 0");
+        if (inv.inputs.size() < 2) raise(MHIP_KERNEL_EXECUTION_FAILED, "missing input at index 1");
+        if (inv.outputs.empty()) raise(MHIP_KERNEL_EXECUTION_FAILED, "missing output at index 0");
+        const std::string& store_id = inv.inputs[0].id;
+        const std::string& rows_id = inv.inputs[1].id;
+        const std::string& out_id = inv.outputs[0].id;
+        auto it = storage.find(store_id);
+        if (it == storage.end())
+            raise(MHIP_KERNEL_EXECUTION_FAILED, "no materialized data for input resource " + store_id);
+        BufferPtr store;
+        if (out_id == store_id) {
+            store = std::move(it->second);
+            storage.erase(it);
+        } else {
+            store = clone(*it->second);
+        }
+        std::string error;
+        mhip_kernel_error code = MHIP_KERNEL_OK;
+        try {
+            auto rit = storage.find(rows_id);
+            if (rit == storage.end())
+                raise(MHIP_KERNEL_EXECUTION_FAILED, "no materialized data for input resource " + rows_id);
+            const Buffer& rows = *rit->second;
+            require_f32(*store, "kv-write");
+            require_f32(rows, "kv-write");
+            const auto [capacity, width] = rows_cols(*store);
+            const auto [count, row_width] = rows_cols(rows);
+            if (row_width != width)
+                raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "kv-write rows have width " +
+                                                         std::to_string(row_width) + ", the store " +
+                                                         std::to_string(width));
+            check(mhip_kv_write_f32(ctx, store->f(), capacity, width, rows.f(), count, *row_offset));
+        } catch (const KernelFailure& f) {
+            code = f.code;
+            error = f.detail;
+        }
+        storage[out_id] = std::move(store);
+        if (code != MHIP_KERNEL_OK) raise(code, error);
+    }
+
     // run_invocation_uncaptured (src/executor.rs:1268-1321): the overwritten
     // output's buffer is offered unless an input reads it; on failure it is
     // put back so the resource keeps its value.
     void run(const Invocation& inv) {
+        if (inv.kernel == "kv-write") {
+            run_kv_write(inv);
+            if (sync_nodes) check(mhip_sync(ctx));
+            return;
+        }
         if (inv.outputs.empty())
             raise(MHIP_KERNEL_EXECUTION_FAILED, "missing output at index 0");
         const std::string& out_id = inv.outputs[0].id;
@@ -939,6 +997,24 @@ mhip_kernel_error mhip_executor_write_zeroed_tensor(mhip_executor* ex, const cha
         auto buf = std::make_unique<Buffer>(ex->ctx, numel(s) * dtype_size(dtype), s, dtype);
         check(mhip_zero(ex->ctx, buf->ptr, buf->bytes));
         ex->storage[id] = std::move(buf);
+    });
+}
+
+mhip_kernel_error mhip_executor_write_zeroed_kv_store(mhip_executor* ex, const char* id,
+                                                      const uint64_t* shape, int rank,
+                                                      int precision, uint64_t head_dimension,
+                                                      int* stored) {
+    (void)head_dimension;  // used by the quantized stores only
+    return guarded([&] {
+        if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
+        if (stored) *stored = 0;
+        if (precision != MHIP_KV_F32) return;
+        Shape s = make_shape(shape, rank);
+        std::lock_guard<std::mutex> lock(ex->mu);
+        auto buf = std::make_unique<Buffer>(ex->ctx, numel(s) * 4, s, MHIP_DTYPE_F32);
+        check(mhip_zero(ex->ctx, buf->ptr, buf->bytes));
+        ex->storage[id] = std::move(buf);
+        if (stored) *stored = 1;
     });
 }
 

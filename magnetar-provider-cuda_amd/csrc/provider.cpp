@@ -55,6 +55,7 @@ const AdvertSpec kAdverts[] = {
     {"add", "add", "Tensor", kF32, 0, ""},
     {"mul", "mul", "Tensor", kF32, 0, ""},
     {"concat", "concat", "Tensor", kF32, 0, ""},
+    {"kv-write", "kv-write", "Tensor", kF32, 2, ""},
     {"residual-add", "residual-add", "Tensor", kF32, 0, ""},
     {"add-half", "add", "Tensor", kHalf, 0, ""},
     {"mul-half", "mul", "Tensor", kHalf, 0, ""},

@@ -16,6 +16,8 @@ import numpy as np
 from . import _lib
 
 F32, F16, BF16 = 0, 1, 2
+# KV store precisions (KvStorePrecision); only KV_F32 stores are provided.
+KV_F32, KV_TQ4, KV_TQ3 = 0, 1, 2
 DTYPE_NAMES = {F32: "Float32", F16: "Float16", BF16: "BrainFloat16"}
 
 KERNEL_ERRORS = {
@@ -96,6 +98,7 @@ _SIGS = {
     "mhip_executor_write_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t], ctypes.c_int),
     "mhip_executor_write_tensor_values": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
     "mhip_executor_write_zeroed_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int], ctypes.c_int),
+    "mhip_executor_write_zeroed_kv_store": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _U64, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "mhip_executor_read_tensor": ([_P, ctypes.c_char_p, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "mhip_executor_read_tensor_values": ([_P, ctypes.c_char_p, _P, ctypes.c_size_t], ctypes.c_int),
     "mhip_executor_read_tensor_rows": ([_P, ctypes.c_char_p, _U64, _U64, _P, ctypes.c_size_t], ctypes.c_int),
@@ -273,6 +276,16 @@ class Executor:
     def write_zeroed_tensor(self, id: str, shape: Sequence[int], dtype: int = F32) -> None:
         shp, rank = _shape(shape)
         _check(_lib_bound().mhip_executor_write_zeroed_tensor(self._h, id.encode(), shp, rank, dtype))
+
+    def write_zeroed_kv_store(self, id: str, shape: Sequence[int], precision: int = KV_F32,
+                              head_dimension: int = 0) -> bool:
+        """A zeroed KV store (src/executor.rs:560-602). True when stored; the
+        quantized precisions are declined (False) and nothing is written."""
+        shp, rank = _shape(shape)
+        stored = ctypes.c_int(0)
+        _check(_lib_bound().mhip_executor_write_zeroed_kv_store(
+            self._h, id.encode(), shp, rank, precision, head_dimension, ctypes.byref(stored)))
+        return bool(stored.value)
 
     def resident_shape(self, id: str):
         shp = (ctypes.c_uint64 * 8)()

@@ -162,3 +162,13 @@ def attention(dev: Device, q: DeviceArray, k: DeviceArray, v: DeviceArray,
     out = _out(dev, out, (rows, params.head_count * params.value_dimension))
     call("mhip_attention_f32", dev.ctx, _p(q), _p(k), _p(v), _p(out), ctypes.byref(params))
     return out
+
+
+def kv_write(dev: Device, store: DeviceArray, rows: DeviceArray, row_offset: int) -> DeviceArray:
+    """store[row_offset : row_offset + len(rows)] = rows, in place (kv-write)."""
+    capacity, width = store.shape
+    count = rows.shape[0] if rows.shape else 0
+    if rows.size != count * width:
+        raise ValueError("kv-write rows must be [count, store width]")
+    call("mhip_kv_write_f32", dev.ctx, _p(store), capacity, width, _p(rows), count, row_offset)
+    return store

@@ -51,7 +51,7 @@ def test_advertisements(provider):
     names = [a.name for a in adverts]
     assert names == ["matmul", "matmul-bias", "matmul-residual", "silu-mul", "gated-matmul",
                      "embedding", "rmsnorm", "rope", "attention", "softmax", "silu", "add", "mul",
-                     "concat", "residual-add", "add-half", "mul-half"]
+                     "concat", "kv-write", "residual-add", "add-half", "mul-half"]
     by = {a.name: a for a in adverts}
     for name in ("matmul", "rope", "attention", "softmax"):
         assert by[name].rank == 2
@@ -278,3 +278,35 @@ def test_observations_and_release(ex):
     assert ex.tensor_count() == n - 1
     ex.copy_tensor("r", "r3")
     assert_bitexact(ex.read_tensor("r3"), np.ones(8, np.float32))
+
+
+def test_kv_write_through_the_executor(ex):
+    """kv-write (src/executor.rs:1366-1420): in place when the output is the
+    store, into a copy otherwise; a failed write leaves the store's rows."""
+    from magnetar_hip import KernelError, Integer
+    from magnetar_hip.executor import KV_F32, KV_TQ4
+    assert ex.write_zeroed_kv_store("kv", (4, 2), KV_F32, 2)
+    ex.write_tensor("kv_rows", np.array([[1, 2], [3, 4]], np.float32))
+    ex.execute(inv("kv-write", ["kv", "kv_rows"], "kv", {"row_offset": Integer(1)}))
+    assert ex.read_tensor("kv").ravel().tolist() == [0, 0, 1, 2, 3, 4, 0, 0]
+    ex.execute(inv("kv-write", ["kv", "kv_rows"], "kv_copy", {"row_offset": Integer(2)}))
+    assert ex.read_tensor("kv_copy").ravel().tolist() == [0, 0, 1, 2, 1, 2, 3, 4]
+    assert ex.read_tensor("kv").ravel().tolist() == [0, 0, 1, 2, 3, 4, 0, 0]
+    ex.write_tensor("kv_wide", np.ones((1, 3), np.float32))
+    cases = [
+        (inv("kv-write", ["kv", "kv_rows"], "kv", {"row_offset": Integer(3)}), "KernelShapeUnsupported"),
+        (inv("kv-write", ["kv", "kv_rows"], "kv", {}), "KernelAttributeUnsupported"),
+        (inv("kv-write", ["kv", "kv_rows"], "kv", {"row_offset": Integer(-1)}), "KernelAttributeUnsupported"),
+        (inv("kv-write", ["kv", "kv_wide"], "kv", {"row_offset": Integer(0)}), "KernelShapeUnsupported"),
+        (inv("kv-write", ["kv", "nothing"], "kv", {"row_offset": Integer(0)}), "KernelExecutionFailed"),
+        (inv("kv-write", ["nothing", "kv_rows"], "kv", {"row_offset": Integer(0)}), "KernelExecutionFailed"),
+    ]
+    for invocation, code in cases:
+        with pytest.raises(KernelError) as err:
+            ex.execute(invocation)
+        assert err.value.code == code, (invocation.attributes, err.value)
+        assert ex.read_tensor("kv").ravel().tolist() == [0, 0, 1, 2, 3, 4, 0, 0]
+    # The quantized stores are declined, and nothing is written.
+    assert not ex.write_zeroed_kv_store("kv_tq", (4, 2), KV_TQ4, 2)
+    with pytest.raises(KernelError):
+        ex.read_tensor("kv_tq")
