@@ -205,6 +205,9 @@ typedef struct {
     uint64_t kv_batch_stride;
     uint64_t v_batch_stride;
     uint64_t out_batch_stride;
+    /* 1 when kv_seq_len came from an explicit key count (the executor's
+     * `key_count` attribute): a captured call may then advance it. */
+    uint32_t bounded_key_count;
 } mhip_attention_params;
 /* q [seq, H*d], k [kv_rows, Hkv*d], v [kv_rows, Hkv*vd] -> out [seq, H*vd].
  * Query i sits at position (kv_seq_len - seq_len) + i; a causal query admits
@@ -220,6 +223,36 @@ mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, co
  * unchanged. An overrun is ShapeUnsupported and writes nothing. */
 mhip_status mhip_kv_write_f32(mhip_ctx* ctx, float* store, uint64_t capacity, uint64_t width,
                               const float* rows, uint64_t count, uint64_t row_offset);
+
+/* ---- step capture and replay (src/kernels.rs:1019-1349, src/executor.rs:177-336) ----
+ * Between mhip_capture_begin and mhip_capture_end, the context's launches are
+ * recorded into a HIP graph instead of running. A launch whose attribute is
+ * named in `advancing` adds the replay offset given to mhip_graph_launch:
+ * RoPE's position_offset, attention's key count (one query row, and only when
+ * the caller sets mhip_attention_params.bounded_key_count) and kv-write's
+ * row_offset. Each such launch bounds the offset (the key count and the rows
+ * written must stay inside K/V and the store). Nothing that allocates,
+ * transfers, clears memory or synchronises can be captured: such a call
+ * returns CaptureUnsupported and fails the capture (mhip_capture_end then
+ * reports the first reason). Multi-row attention replays only at offset 0. */
+typedef enum {
+    MHIP_ADVANCE_POSITION_OFFSET = 1,
+    MHIP_ADVANCE_KEY_COUNT = 2,
+    MHIP_ADVANCE_ROW_OFFSET = 4
+} mhip_advancing;
+typedef struct mhip_graph mhip_graph;
+mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing);
+/* Instantiates the recorded step; *max_offset is the largest replay offset
+ * every advancing launch allows. Does not run it. */
+mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offset);
+mhip_status mhip_capture_abort(mhip_ctx* ctx);
+int mhip_capture_active(const mhip_ctx* ctx);
+/* Runs the step with every advancing attribute increased by `offset`
+ * (ShapeUnsupported beyond the bound). The failure flags are cleared at the
+ * start of every run. */
+mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset);
+uint64_t mhip_graph_max_offset(const mhip_graph* graph);
+mhip_status mhip_graph_destroy(mhip_graph* graph);
 
 /* ---- decoder block, chained device-resident (src/tests_hardware_hot_path.rs:339-526) ---- */
 typedef struct {
@@ -287,7 +320,9 @@ typedef enum {
     MHIP_KERNEL_EXECUTION_FAILED = 6,
     MHIP_KERNEL_ATTRIBUTE_UNSUPPORTED = 7,
     MHIP_KERNEL_NOT_FOUND = 8,
-    MHIP_KERNEL_TIMEOUT = 9
+    MHIP_KERNEL_TIMEOUT = 9,
+    /* replay_step only: StepReplayError::Invalidated (src/executor.rs:272-336) */
+    MHIP_STEP_REPLAY_INVALIDATED = 10
 } mhip_kernel_error;
 
 /* `OperatorAttributeValue` (src/executor.rs:1141-1185). */
@@ -397,6 +432,25 @@ mhip_kernel_error mhip_executor_complete_kernel(mhip_executor* ex, uint64_t hand
 /* submit + complete in one call. */
 mhip_kernel_error mhip_executor_execute(mhip_executor* ex, const mhip_invocation* inv);
 /* MAGNETAR_HIP_SYNC_NODES equivalent: wait for the device after each dispatch. */
+/* Step capture (src/executor.rs:177-336): the invocations between begin and
+ * end are recorded into a HIP graph (see mhip_capture_begin); `advancing`
+ * names the attributes a replay offset increases ("position_offset",
+ * "key_count", "row_offset"). end instantiates the step, runs it once and
+ * writes its id ("<provider>:step-capture:<n>"). replay_step writes each
+ * input's f32 values into the buffer the step read and runs it at `offset`:
+ * MHIP_STEP_REPLAY_INVALIDATED when a captured resource has another buffer
+ * now, an input was not read by the step or the offset leaves the bounds;
+ * MHIP_KERNEL_EXECUTION_FAILED for an invalid embedding id. */
+int mhip_executor_supports_step_capture(mhip_executor* ex);
+mhip_kernel_error mhip_executor_begin_step_capture(mhip_executor* ex, const char* const* advancing,
+                                                   int count);
+mhip_kernel_error mhip_executor_end_step_capture(mhip_executor* ex, char* id_out, size_t capacity);
+mhip_kernel_error mhip_executor_abort_step_capture(mhip_executor* ex);
+mhip_kernel_error mhip_executor_replay_step(mhip_executor* ex, const char* id, uint64_t offset,
+                                            const char* const* input_ids,
+                                            const float* const* input_values,
+                                            const uint64_t* input_lengths, int input_count);
+mhip_kernel_error mhip_executor_release_step_capture(mhip_executor* ex, const char* id);
 mhip_status mhip_executor_set_sync_nodes(mhip_executor* ex, int enabled);
 /* The observation log (last 4096 entries, src/executor.rs:82). */
 uint64_t mhip_executor_observation_count(mhip_executor* ex);

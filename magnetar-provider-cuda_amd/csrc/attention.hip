@@ -34,6 +34,7 @@
 //    softmax over 64-key chunks.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace {
@@ -53,7 +54,18 @@ struct AttnArgs {
     int64_t window;        // -1: none
     float qscale;          // scale * log2(e), applied to q
     uint64_t q_bs, k_bs, v_bs, o_bs;  // batch strides (floats)
+    const uint64_t* advance;  // captured step: replay offset added to the key count
 };
+
+// A captured step's replay offset moves the key count, and with it the
+// queries' positions (src/kernels.rs:1425-1435).
+__device__ __forceinline__ void apply_advance(AttnArgs& a) {
+    if (a.advance) {
+        const uint64_t d = *a.advance;
+        a.kv_seq += d;
+        a.offset += d;
+    }
+}
 
 // Admitted key range of the query at position qpos (src/kernels.cu:1909-1920).
 __device__ __forceinline__ void key_range(const AttnArgs& a, uint64_t qpos, uint64_t* lo,
@@ -90,6 +102,7 @@ struct PrefillCfg {
 
 template <int D, int VD>
 __global__ __launch_bounds__(256, (D > 64 ? 1 : 2)) void attn_prefill_kernel(AttnArgs a) {
+    apply_advance(a);
     using Cfg = PrefillCfg<D, VD>;
     extern __shared__ float lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -306,7 +319,7 @@ __host__ __device__ constexpr int decode_chunk(int d4) { return decode_steps(d4)
 // chunk max (log2 domain) and weight sum.
 template <int D4, int GT>
 __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
-    AttnArgs a, uint64_t key_lo, uint64_t key_hi, uint64_t chunks, float* __restrict__ part_o,
+    AttnArgs a, uint64_t key_base, uint64_t chunks, float* __restrict__ part_o,
     float* __restrict__ part_ml) {
     constexpr int kLPK = D4;              // lanes per key
     constexpr int kKPS = 64 / kLPK;       // keys per wave step
@@ -325,8 +338,15 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     const uint64_t c_idx = blockIdx.x / units;
     const uint64_t bkv = blockIdx.x % units;
     const uint64_t kvh = bkv % a.kv_heads, b = bkv / a.kv_heads;
-    const uint64_t c_lo = key_lo + c_idx * static_cast<uint64_t>(kSteps * kKPW);
-    const int n = c_lo < key_hi ? static_cast<int>(min<uint64_t>(key_hi - c_lo, kSteps * kKPW)) : 0;
+    // The chunk's keys: [key_base + c * chunk, + chunk) inside the admitted
+    // range of the query (at position offset; a replay may move it).
+    apply_advance(a);
+    uint64_t key_lo, key_hi;
+    key_range(a, a.offset, &key_lo, &key_hi);
+    const uint64_t c_base = key_base + c_idx * static_cast<uint64_t>(kSteps * kKPW);
+    const uint64_t c_lo = max(c_base, key_lo);
+    const uint64_t c_hi = min(c_base + static_cast<uint64_t>(kSteps * kKPW), key_hi);
+    const int n = c_lo < c_hi ? static_cast<int>(c_hi - c_lo) : 0;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / kLPK, sl = lane % kLPK;
@@ -513,29 +533,23 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
 }
 
 mhip_status attention_workspace(mhip_ctx* ctx, size_t bytes, float** out) {
-    if (ctx->workspace_bytes < bytes) {
-        if (ctx->workspace) {
-            (void)hipStreamSynchronize(ctx->stream);
-            (void)hipFree(ctx->workspace);
-            ctx->workspace = nullptr;
-            ctx->workspace_bytes = 0;
-        }
-        hipError_t err = hipMalloc(&ctx->workspace, bytes);
-        if (err != hipSuccess) return mhip::from_hip(err, "allocating the attention workspace");
-        ctx->workspace_bytes = bytes;
-    }
-    *out = static_cast<float*>(ctx->workspace);
-    return MHIP_OK;
+    void* p = nullptr;
+    mhip_status st = mhip::workspace(ctx, bytes, &p);
+    *out = static_cast<float*>(p);
+    return st;
 }
 
 template <int D4, int GT>
-mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
+mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch,
+                                uint64_t kv_rows, bool bounded) {
     constexpr int D = 4 * D4;
     constexpr uint64_t kChunk = decode_chunk(D4);
     // The one query (seq == 1) sits at position kv_seq - 1 in every batch
     // row and head, so the admitted key range is the same for all of them.
-    uint64_t lo, hi;
-    {
+    // A captured call whose key count advances covers every row of K/V; its
+    // workgroups find their keys from the replayed count.
+    uint64_t lo = 0, hi = kv_rows;
+    if (!a.advance) {
         uint64_t upper = a.causal ? a.offset + 1 : a.kv_seq;
         if (upper > a.kv_seq) upper = a.kv_seq;
         uint64_t lower = 0;
@@ -554,13 +568,17 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
     if (units * chunks >= (1ULL << 31))
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention decode: too many key chunks");
     const uint64_t records = batch * a.heads * chunks;
+    // A call bounded by a key count sizes the scratch for every row of K/V,
+    // so a step captured later at the same shape never needs to grow it.
+    const uint64_t reserve = bounded ? batch * a.heads * std::max<uint64_t>(1, (kv_rows + kChunk - 1) / kChunk)
+                                     : records;
     float* part = nullptr;
-    mhip_status st = attention_workspace(ctx, records * (D + 2) * sizeof(float), &part);
+    mhip_status st = attention_workspace(ctx, std::max(records, reserve) * (D + 2) * sizeof(float), &part);
     if (st != MHIP_OK) return st;
     float* part_o = part;
     float* part_ml = part + records * D;
     hipLaunchKernelGGL((attn_decode_partial_kernel<D4, GT>), dim3(static_cast<unsigned>(units * chunks)),
-                       dim3(256), 0, ctx->stream, a, lo, hi, chunks, part_o, part_ml);
+                       dim3(256), 0, ctx->stream, a, lo, chunks, part_o, part_ml);
     st = mhip::check_launch("attention (decode chunks)");
     if (st != MHIP_OK) return st;
     hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
@@ -569,12 +587,13 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
 }
 
 template <int D4>
-mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
+mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch, uint64_t kv_rows,
+                          bool bounded) {
     const uint64_t group = a.heads / a.kv_heads;
-    if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch);
-    if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch);
-    if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch);
-    return launch_decode_group<D4, 8>(ctx, a, batch);
+    if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch, kv_rows, bounded);
+    if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch, kv_rows, bounded);
+    if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch, kv_rows, bounded);
+    return launch_decode_group<D4, 8>(ctx, a, batch, kv_rows, bounded);
 }
 
 // ---------------------------------------------------------------------------
@@ -582,6 +601,7 @@ mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, uint64_t total) {
+    apply_advance(a);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t item = static_cast<uint64_t>(blockIdx.x) * 4 + wave;
     if (item >= total) return;
@@ -691,6 +711,15 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
     a.window = p->window_size > 0 ? p->window_size : -1;
     const float scale = p->scale > 0.0f ? p->scale : 1.0f / std::sqrt(static_cast<float>(d));
     a.qscale = scale * kLog2e;
+    // A captured call bounded by an explicit key count advances it with the
+    // replay offset (one query row; several rows replay only at offset 0).
+    a.advance = nullptr;
+    if (p->bounded_key_count) {
+        if (p->seq_len == 1)
+            a.advance = mhip::advance_ptr(ctx, MHIP_ADVANCE_KEY_COUNT, p->kv_rows - p->kv_seq_len);
+        else
+            (void)mhip::advance_ptr(ctx, MHIP_ADVANCE_KEY_COUNT, 0);
+    }
     a.q_bs = p->q_batch_stride ? p->q_batch_stride : p->seq_len * H * d;
     a.k_bs = p->kv_batch_stride ? p->kv_batch_stride : p->kv_rows * Hkv * d;
     a.v_bs = p->v_batch_stride ? p->v_batch_stride : p->kv_rows * Hkv * vd;
@@ -703,13 +732,13 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
         p->kv_seq_len > 0) {
         mhip_status st = MHIP_CAPTURE_UNSUPPORTED;
         switch (d / 4) {
-            case 1: st = launch_decode<1>(ctx, a, batch); break;
-            case 2: st = launch_decode<2>(ctx, a, batch); break;
-            case 4: st = launch_decode<4>(ctx, a, batch); break;
-            case 8: st = launch_decode<8>(ctx, a, batch); break;
-            case 16: st = launch_decode<16>(ctx, a, batch); break;
-            case 32: st = launch_decode<32>(ctx, a, batch); break;
-            case 64: st = launch_decode<64>(ctx, a, batch); break;
+            case 1: st = launch_decode<1>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 2: st = launch_decode<2>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 4: st = launch_decode<4>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 8: st = launch_decode<8>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 16: st = launch_decode<16>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 32: st = launch_decode<32>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
+            case 64: st = launch_decode<64>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;
             default: break;
         }
         if (st != MHIP_CAPTURE_UNSUPPORTED) return st;  // else: no decode kernel for this d

@@ -28,6 +28,23 @@ struct mhip_ctx {
     // Grow-only device workspace for split-k partial sums (matmul, attention).
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+
+    // Step capture: while `capturing`, launches on the stream are recorded
+    // into a HIP graph instead of running. Launches whose attribute is in
+    // `advancing` (MHIP_ADVANCE_* bits) add the replay offset read from the
+    // device word `offset`; each records how far it may advance in
+    // `max_offset`. `failure` keeps the first reason the capture cannot be
+    // replayed (an allocation, a transfer, a synchronisation).
+    bool capturing = false;
+    uint32_t advancing = 0;
+    uint64_t* capture_offset = nullptr;
+    uint64_t max_offset = 0;
+    std::string capture_failure;
+    std::vector<void*> deferred_frees;  // mhip_free calls made while capturing
+    // Graphs alive on this context; while any is, buffers it may read (the
+    // workspace, RoPE tables) are retired instead of freed.
+    int live_graphs = 0;
+    std::vector<void*> retired;
 };
 
 namespace mhip {
@@ -102,6 +119,22 @@ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // Checks the launch that was just enqueued.
 mhip_status check_launch(const char* what);
+
+// While capturing: records that `what` cannot be captured (the first such
+// reason fails the capture) and returns MHIP_CAPTURE_UNSUPPORTED. MHIP_OK
+// otherwise.
+mhip_status forbid_in_capture(mhip_ctx* ctx, const char* what);
+
+// While capturing a launch whose attribute `bit` (MHIP_ADVANCE_*) advances:
+// the device address of the replay offset, after recording that this launch
+// stays in bounds for offsets up to `max_offset`. nullptr otherwise (no
+// offset is added).
+const uint64_t* advance_ptr(mhip_ctx* ctx, uint32_t bit, uint64_t max_offset);
+
+// The context's grow-only scratch of at least `bytes` (split-k partials,
+// attention chunk records). Growing it waits for the stream; a buffer a live
+// graph may read is retired, not freed. Refused while capturing.
+mhip_status workspace(mhip_ctx* ctx, size_t bytes, void** out);
 
 // The device (frequency, amplitude) table of a RoPE call's pairs, computed
 // on the host with the f32 operations of src/kernels.cu:1197-1221 and cached

@@ -101,11 +101,17 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     rope[1].head_count = c.kv_heads;
     // Decode (a few rows): Q, K, V as one set of GEMVs with RoPE applied where
     // their split-k sums are added. Otherwise three matmuls and two RoPE calls.
-    const mhip::GemvTarget qkv[3] = {{w->wq, c.heads * c.head_dim, q},
-                                     {w->wk, kv_dim, k_rows},
-                                     {w->wv, kv_dim, v_rows}};
+    // In a captured step whose row offset advances, the K/V rows written
+    // follow the replay offset (the rows left below them bound it).
+    const uint64_t rows_left = cache_rows - (position + seq);
+    mhip::GemvTarget qkv[3] = {{w->wq, c.heads * c.head_dim, q},
+                               {w->wk, kv_dim, k_rows, true, rows_left},
+                               {w->wv, kv_dim, v_rows, true, rows_left}};
     st = mhip::gemv_set_f32(ctx, h, seq, c.hidden, qkv, 3, mhip::kGemvRopeQK, rope);
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        // The separate matmuls write fixed rows of the cache.
+        if (mhip::capture_advancing(ctx) & MHIP_ADVANCE_ROW_OFFSET)
+            return mhip::forbid_in_capture(ctx, "a K/V append of more than 8 rows with an advancing row offset");
         MHIP_TRY(mhip_matmul_f32(ctx, h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, 0, 0, nullptr, 0));
         MHIP_TRY(mhip_matmul_f32(ctx, h, w->wk, k_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
         MHIP_TRY(mhip_matmul_f32(ctx, h, w->wv, v_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
@@ -124,6 +130,7 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     ap.head_dimension = c.head_dim;
     ap.value_dimension = c.head_dim;
     ap.causal = 1;
+    ap.bounded_key_count = 1;
     ap.window_size = -1;
     ap.batch = 1;
     MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));

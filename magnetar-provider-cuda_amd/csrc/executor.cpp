@@ -27,6 +27,7 @@
 #include <tuple>
 #include <vector>
 
+#include "internal.hpp"
 #include "magnetar_hip.h"
 
 namespace {
@@ -192,8 +193,25 @@ struct Observation {
 
 }  // namespace
 
+// What a step capture read and wrote (src/executor.rs:339-380): each
+// resource's buffer as captured, and the vocabulary of every embedding
+// lookup's ids, which a replay checks on the host.
+struct Recording {
+    std::map<std::string, std::pair<void*, size_t>> resources;
+    std::map<std::string, uint64_t> embedding_ids;
+    bool has_embedding = false;
+};
+
+struct CapturedStep {
+    mhip_graph* graph = nullptr;
+    Recording recording;
+};
+
 struct mhip_executor {
     mhip_ctx* ctx = nullptr;
+    std::unique_ptr<Recording> capture;  // while a step capture is recording
+    std::map<std::string, CapturedStep> captures;
+    uint64_t next_capture = 0;
     std::string device_id, provider_name;
     std::mutex mu;
     std::map<std::string, BufferPtr> storage;
@@ -313,8 +331,15 @@ struct mhip_executor {
         const uint64_t num = numel(ids.shape);
         BufferPtr out = alloc_output(offered, Shape{num, dim}, MHIP_DTYPE_F32);
         check(mhip_embedding_f32(ctx, table.f(), vocab, dim, ids.f(), num, out->f()));
-        mhip_status st = mhip_check_flags(ctx, nullptr);
-        if (st != MHIP_OK) raise(map_status(st), mhip_last_error_detail());
+        if (capture) {
+            // A captured step checks its ids on the host at each replay and
+            // the flag after its first run.
+            capture->has_embedding = true;
+            capture->embedding_ids[inv.inputs[1].id] = vocab;
+        } else {
+            mhip_status st = mhip_check_flags(ctx, nullptr);
+            if (st != MHIP_OK) raise(map_status(st), mhip_last_error_detail());
+        }
         if (factor) check(mhip_scale_f32(ctx, out->f(), out->f(), *factor, num * dim));
         return out;
     }
@@ -482,6 +507,8 @@ struct mhip_executor {
 
     // src/kernels.rs:4357-4386.
     BufferPtr op_softmax(const Buffer& x, BufferPtr& offered) {
+        // Its failure check reads the device (src/kernels.rs:4360).
+        check(mhip::forbid_in_capture(ctx, "softmax"));
         require_f32(x, "softmax");
         auto [rows, cols] = rows_cols(x);
         BufferPtr out = alloc_output(offered, x.shape, MHIP_DTYPE_F32);
@@ -657,6 +684,7 @@ struct mhip_executor {
         p.window_size = window ? static_cast<int64_t>(*window) : -1;
         p.scale = scale.value_or(0.0f);
         p.batch = 1;
+        p.bounded_key_count = key_count.has_value() ? 1 : 0;
         BufferPtr out = alloc_output(offered, Shape{seq, H * vd}, MHIP_DTYPE_F32);
         check(mhip_attention_f32(ctx, q.f(), k.f(), v.f(), out->f(), &p));
         return out;
@@ -686,6 +714,7 @@ struct mhip_executor {
 
     // add-half / mul-half on 2-byte device buffers (src/executor.rs:1970-2013).
     BufferPtr op_half(const Invocation& inv, bool mul, BufferPtr& offered) {
+        check(mhip::forbid_in_capture(ctx, "a half-precision Kernel"));
         const Buffer& a = get(inv, 0);
         const Buffer& b = get(inv, 1);
         const int dtype = inv.inputs[0].dtype;
@@ -810,7 +839,8 @@ struct mhip_executor {
     void run(const Invocation& inv) {
         if (inv.kernel == "kv-write") {
             run_kv_write(inv);
-            if (sync_nodes) check(mhip_sync(ctx));
+            record(inv);
+            if (sync_nodes && !capture) check(mhip_sync(ctx));
             return;
         }
         if (inv.outputs.empty())
@@ -833,7 +863,19 @@ struct mhip_executor {
             if (offered) storage[out_id] = std::move(offered);
             throw;
         }
-        if (sync_nodes) check(mhip_sync(ctx));
+        record(inv);
+        if (sync_nodes && !capture) check(mhip_sync(ctx));
+    }
+
+    // Notes the buffers a captured invocation read and wrote.
+    void record(const Invocation& inv) {
+        if (!capture) return;
+        auto note = [&](const TensorRef& r) {
+            auto it = storage.find(r.id);
+            if (it != storage.end()) capture->resources[r.id] = {it->second->ptr, it->second->bytes};
+        };
+        for (const auto& r : inv.inputs) note(r);
+        for (const auto& r : inv.outputs) note(r);
     }
 
     // execute_invocation (src/executor.rs:1191-1233).
@@ -937,6 +979,12 @@ mhip_status mhip_executor_destroy(mhip_executor* ex) {
     if (!ex) return MHIP_OK;
     {
         std::lock_guard<std::mutex> lock(ex->mu);
+        if (ex->capture) {
+            mhip_capture_abort(ex->ctx);
+            ex->capture.reset();
+        }
+        for (auto& entry : ex->captures) mhip_graph_destroy(entry.second.graph);
+        ex->captures.clear();
         mhip_sync(ex->ctx);
         ex->storage.clear();
     }
@@ -1184,6 +1232,129 @@ mhip_status mhip_executor_observation(mhip_executor* ex, uint64_t index, mhip_ob
     std::snprintf(out->invocation, sizeof(out->invocation), "%s", o.invocation.c_str());
     out->error = o.error;
     return MHIP_OK;
+}
+
+// ---- step capture (src/executor.rs:177-336) ----
+
+int mhip_executor_supports_step_capture(mhip_executor* ex) { return ex ? 1 : 0; }
+
+mhip_kernel_error mhip_executor_begin_step_capture(mhip_executor* ex, const char* const* advancing,
+                                                   int count) {
+    return guarded([&] {
+        if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        if (ex->capture) raise(MHIP_KERNEL_EXECUTION_FAILED, "a step capture is already in progress");
+        uint32_t bits = 0;
+        for (int i = 0; i < count; ++i) {
+            const std::string name = advancing && advancing[i] ? advancing[i] : "";
+            if (name == "position_offset") bits |= MHIP_ADVANCE_POSITION_OFFSET;
+            else if (name == "key_count") bits |= MHIP_ADVANCE_KEY_COUNT;
+            else if (name == "row_offset") bits |= MHIP_ADVANCE_ROW_OFFSET;
+        }
+        mhip_status st = mhip_capture_begin(ex->ctx, bits);
+        if (st != MHIP_OK) raise(MHIP_KERNEL_EXECUTION_FAILED, mhip_last_error_detail());
+        ex->capture = std::make_unique<Recording>();
+    });
+}
+
+// Instantiates the recorded step and runs it once, so its results are
+// available; writes the step's id to `id_out`.
+mhip_kernel_error mhip_executor_end_step_capture(mhip_executor* ex, char* id_out, size_t capacity) {
+    return guarded([&] {
+        if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        if (!ex->capture) raise(MHIP_KERNEL_EXECUTION_FAILED, "no step capture is in progress");
+        std::unique_ptr<Recording> recording = std::move(ex->capture);
+        mhip_graph* graph = nullptr;
+        uint64_t max_offset = 0;
+        mhip_status st = mhip_capture_end(ex->ctx, &graph, &max_offset);
+        if (st != MHIP_OK) raise(MHIP_KERNEL_EXECUTION_FAILED, mhip_last_error_detail());
+        st = mhip_graph_launch(graph, 0);
+        if (st == MHIP_OK && recording->has_embedding) st = mhip_check_flags(ex->ctx, nullptr);
+        if (st != MHIP_OK) {
+            const std::string detail = mhip_last_error_detail();
+            mhip_graph_destroy(graph);
+            raise(MHIP_KERNEL_EXECUTION_FAILED, detail);
+        }
+        const std::string id = ex->provider_name + ":step-capture:" + std::to_string(ex->next_capture++);
+        ex->captures[id] = CapturedStep{graph, std::move(*recording)};
+        if (id_out && capacity) std::snprintf(id_out, capacity, "%s", id.c_str());
+    });
+}
+
+mhip_kernel_error mhip_executor_abort_step_capture(mhip_executor* ex) {
+    return guarded([&] {
+        if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        ex->capture.reset();
+        mhip_capture_abort(ex->ctx);
+    });
+}
+
+// Runs a captured step again with every advancing attribute increased by
+// `offset`, after writing `inputs` into the buffers the step reads. A step
+// whose buffers moved, or an input it never read, is Invalidated; an invalid
+// embedding id fails the replay before anything runs.
+mhip_kernel_error mhip_executor_replay_step(mhip_executor* ex, const char* id, uint64_t offset,
+                                            const char* const* input_ids,
+                                            const float* const* input_values,
+                                            const uint64_t* input_lengths, int input_count) {
+    return guarded([&] {
+        if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        auto it = ex->captures.find(id);
+        if (it == ex->captures.end())
+            raise(MHIP_STEP_REPLAY_INVALIDATED, std::string("no step capture '") + id + "'");
+        CapturedStep& step = it->second;
+        const uint64_t bound = mhip_graph_max_offset(step.graph);
+        if (offset > bound)
+            raise(MHIP_STEP_REPLAY_INVALIDATED, "offset " + std::to_string(offset) +
+                                                    " leaves the captured bounds (at most " +
+                                                    std::to_string(bound) + ")");
+        for (const auto& [resource, where] : step.recording.resources) {
+            auto s = ex->storage.find(resource);
+            if (s == ex->storage.end() || s->second->ptr != where.first || s->second->bytes != where.second)
+                raise(MHIP_STEP_REPLAY_INVALIDATED,
+                      "resource '" + resource + "' no longer has its captured storage");
+        }
+        for (int i = 0; i < input_count; ++i) {
+            const std::string resource = input_ids[i] ? input_ids[i] : "";
+            if (!step.recording.resources.count(resource))
+                raise(MHIP_STEP_REPLAY_INVALIDATED,
+                      "input '" + resource + "' was not read by the captured step");
+            auto vocab = step.recording.embedding_ids.find(resource);
+            if (vocab != step.recording.embedding_ids.end()) {
+                for (uint64_t j = 0; j < input_lengths[i]; ++j) {
+                    const float value = input_values[i][j];
+                    if (!(value >= 0.0f && value == std::floor(value) &&
+                          static_cast<double>(value) < static_cast<double>(vocab->second)))
+                        raise(MHIP_KERNEL_EXECUTION_FAILED,
+                              "embedding lookup id is not a valid in-range non-negative integer");
+                }
+            }
+        }
+        for (int i = 0; i < input_count; ++i) {
+            Buffer& buffer = *ex->storage[input_ids[i]];
+            if (buffer.dtype != MHIP_DTYPE_F32 || input_lengths[i] * 4 != buffer.bytes)
+                raise(MHIP_KERNEL_EXECUTION_FAILED,
+                      std::string("replay input '") + input_ids[i] + "' has " +
+                          std::to_string(input_lengths[i]) + " values, its buffer " +
+                          std::to_string(buffer.bytes / 4));
+            check(mhip_upload(ex->ctx, buffer.ptr, input_values[i], buffer.bytes));
+        }
+        check(mhip_graph_launch(step.graph, offset));
+    });
+}
+
+mhip_kernel_error mhip_executor_release_step_capture(mhip_executor* ex, const char* id) {
+    return guarded([&] {
+        if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        auto it = ex->captures.find(id);
+        if (it == ex->captures.end()) return;
+        mhip_graph_destroy(it->second.graph);
+        ex->captures.erase(it);
+    });
 }
 
 }  // extern "C"

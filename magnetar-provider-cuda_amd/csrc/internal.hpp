@@ -28,6 +28,10 @@ struct GemvTarget {
     const float* b;
     uint64_t n;
     float* out;
+    // While capturing with MHIP_ADVANCE_ROW_OFFSET: the rows written move
+    // down by the replay offset (a KV cache append), by at most this many.
+    bool row_advances = false;
+    uint64_t row_advance_limit = 0;
 };
 
 // Epilogues applied where the split-k partial sums are added up.
@@ -47,5 +51,12 @@ enum GemvEpilogue : int {
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                          const GemvTarget* targets, int count, int epilogue,
                          const mhip_rope_params* rope);
+
+// While capturing: records that `what` cannot be captured and returns
+// MHIP_CAPTURE_UNSUPPORTED; MHIP_OK otherwise.
+mhip_status forbid_in_capture(mhip_ctx* ctx, const char* what);
+
+// The MHIP_ADVANCE_* bits of the capture in progress (0 when not capturing).
+uint32_t capture_advancing(const mhip_ctx* ctx);
 
 }  // namespace mhip

@@ -6,16 +6,28 @@
 
 namespace {
 
+// dst row = row_offset (+ the replay offset of a captured step).
+__device__ __forceinline__ uint64_t first_row(uint64_t row_offset, const uint64_t* advance) {
+    return row_offset + (advance ? *advance : 0);
+}
+
 __global__ __launch_bounds__(256) void kv_write_vec_kernel(const float4* __restrict__ rows,
-                                                           float4* __restrict__ dst, uint64_t n4) {
+                                                           float* __restrict__ store,
+                                                           uint64_t width, uint64_t row_offset,
+                                                           const uint64_t* advance, uint64_t n4) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n4) dst[i] = rows[i];
+    if (i >= n4) return;
+    float4* dst = reinterpret_cast<float4*>(store + first_row(row_offset, advance) * width);
+    dst[i] = rows[i];
 }
 
 __global__ __launch_bounds__(256) void kv_write_scalar_kernel(const float* __restrict__ rows,
-                                                              float* __restrict__ dst, uint64_t n) {
+                                                              float* __restrict__ store,
+                                                              uint64_t width, uint64_t row_offset,
+                                                              const uint64_t* advance, uint64_t n) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n) dst[i] = rows[i];
+    if (i >= n) return;
+    store[first_row(row_offset, advance) * width + i] = rows[i];
 }
 
 }  // namespace
@@ -29,18 +41,20 @@ extern "C" mhip_status mhip_kv_write_f32(mhip_ctx* ctx, float* store, uint64_t c
                           "kv-write of " + std::to_string(count) + " rows at " +
                               std::to_string(row_offset) + " exceeds the store's " +
                               std::to_string(capacity) + " rows");
+    // A captured write may move down by up to the rows left after it.
+    const uint64_t* advance =
+        mhip::advance_ptr(ctx, MHIP_ADVANCE_ROW_OFFSET, capacity - (row_offset + count));
     const uint64_t n = count * width;
     if (n == 0) return MHIP_OK;
     if (!store || !rows) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "kv-write: null buffer");
-    float* dst = store + row_offset * width;
-    if (n % 4 == 0 && mhip::aligned16(dst) && mhip::aligned16(rows)) {
+    if (n % 4 == 0 && width % 4 == 0 && mhip::aligned16(store) && mhip::aligned16(rows)) {
         const uint64_t n4 = n / 4;
         hipLaunchKernelGGL(kv_write_vec_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
-                           dim3(256), 0, ctx->stream, reinterpret_cast<const float4*>(rows),
-                           reinterpret_cast<float4*>(dst), n4);
+                           dim3(256), 0, ctx->stream, reinterpret_cast<const float4*>(rows), store,
+                           width, row_offset, advance, n4);
     } else {
         hipLaunchKernelGGL(kv_write_scalar_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-                           dim3(256), 0, ctx->stream, rows, dst, n);
+                           dim3(256), 0, ctx->stream, rows, store, width, row_offset, advance, n);
     }
     return mhip::check_launch("kv-write");
 }

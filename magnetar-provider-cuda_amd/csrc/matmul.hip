@@ -35,22 +35,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kGemvMaxRows = 8;
 
-// Grow-only scratch for split-k partial sums, kept on the context; stream
-// order makes reuse by the next call safe.
+// Split-k partial sums live in the context's workspace; stream order makes
+// reuse by the next call safe.
 mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
-    if (ctx->workspace_bytes < bytes) {
-        if (ctx->workspace) {
-            (void)hipStreamSynchronize(ctx->stream);
-            (void)hipFree(ctx->workspace);
-            ctx->workspace = nullptr;
-            ctx->workspace_bytes = 0;
-        }
-        hipError_t err = hipMalloc(&ctx->workspace, bytes);
-        if (err != hipSuccess) return mhip::from_hip(err, "allocating the matmul workspace");
-        ctx->workspace_bytes = bytes;
-    }
-    *out = static_cast<float*>(ctx->workspace);
-    return MHIP_OK;
+    void* p = nullptr;
+    mhip_status st = mhip::workspace(ctx, bytes, &p);
+    *out = static_cast<float*>(p);
+    return st;
 }
 
 // ---------------------------------------------------------------------------
@@ -527,6 +518,7 @@ struct GemvSeg {
     const float* b;
     float* partial;
     float* out;
+    const uint64_t* out_advance;  // captured step: rows of `out` move by the replay offset
     uint64_t n;
     uint64_t k_per_slice;
     uint32_t col_groups, slices;
@@ -545,6 +537,7 @@ struct RopeEpi {
     const float* table;  // [half] frequencies then [half] amplitudes
     uint64_t head_width, dimension, half, offset;
     float scale;
+    const uint64_t* advance;  // captured step: replay offset added to `offset`
 };
 
 // Segment `i` of the set with constant indices, so the fields stay in the
@@ -571,7 +564,8 @@ __device__ __forceinline__ float4 rope_vec(const RopeEpi& e, uint64_t row, uint6
     const uint64_t j = col % e.head_width;
     if (j >= e.dimension) return v;
     const uint64_t p = j / 2;
-    const float position = mhip::rope_position(e.offset, row, e.scale);
+    const uint64_t offset = e.offset + (e.advance ? *e.advance : 0);
+    const float position = mhip::rope_position(offset, row, e.scale);
     float c0, s0, c1, s1;
     mhip::rope_pair_cs(position, e.table, e.half, p, &c0, &s0);
     mhip::rope_pair_cs(position, e.table, e.half, p + 1, &c1, &s1);
@@ -601,6 +595,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
         __syncthreads();
         gemv_reduce_sum<ROWS>(u.partial, u.n, u.slices, col, live, w);
         if (wave != 0 || !live) return;
+        float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0);
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             float4 o;
@@ -608,16 +603,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
             o.y = mhip::silu1(v[r].y) * w[r].y;
             o.z = mhip::silu1(v[r].z) * w[r].z;
             o.w = mhip::silu1(v[r].w) * w[r].w;
-            *reinterpret_cast<float4*>(s.out + r * s.n + col) = o;
+            *reinterpret_cast<float4*>(out + r * s.n + col) = o;
         }
         return;
     }
     if (wave != 0 || !live) return;
+    float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         float4 o = v[r];
         if (epilogue == mhip::kGemvRopeQK && i < 2) o = rope_vec(i == 0 ? rope_q : rope_k, r, col, o);
-        *reinterpret_cast<float4*>(s.out + r * s.n + col) = o;
+        *reinterpret_cast<float4*>(out + r * s.n + col) = o;
     }
 }
 
@@ -761,6 +757,9 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
         gemv_slicing(ctx, k, t.n, &slices, &k_per_slice);
         g.b = t.b;
         g.out = t.out;
+        g.out_advance = t.row_advances
+                            ? advance_ptr(ctx, MHIP_ADVANCE_ROW_OFFSET, t.row_advance_limit)
+                            : nullptr;
         g.n = t.n;
         g.k_per_slice = k_per_slice;
         g.col_groups = static_cast<uint32_t>((t.n + kGemvCols - 1) / kGemvCols);
@@ -795,11 +794,13 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
             e.half = q.dimension / 2;
             e.offset = q.position_offset;
             e.scale = q.scale;
+            e.advance = advance_ptr(ctx, MHIP_ADVANCE_POSITION_OFFSET, UINT64_MAX);
         }
     }
-    float* partial = nullptr;
-    mhip_status st = workspace(ctx, floats * sizeof(float), &partial);
+    void* scratch = nullptr;
+    mhip_status st = workspace(ctx, floats * sizeof(float), &scratch);
     if (st != MHIP_OK) return st;
+    float* partial = static_cast<float*>(scratch);
     for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
     const uint32_t g = static_cast<uint32_t>(groups);
     switch (rows) {

@@ -63,8 +63,11 @@ mhip_status device_table(mhip_ctx* ctx, const std::vector<float>& table, const f
             return MHIP_OK;
         }
     }
-    if (ctx->rope_tables.size() >= 16) {
-        // Wait for kernels that may still read the oldest table, then drop it.
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a host-to-device upload"); st != MHIP_OK)
+        return st;
+    if (ctx->rope_tables.size() >= 16 && ctx->live_graphs == 0) {
+        // Wait for kernels that may still read the oldest table, then drop it
+        // (never while a captured step may read it).
         (void)hipStreamSynchronize(ctx->stream);
         (void)hipFree(ctx->rope_tables.front().device);
         ctx->rope_tables.erase(ctx->rope_tables.begin());
@@ -108,11 +111,13 @@ struct RopeArgs {
     const float* table;  // [half] frequencies then [half] amplitudes
     uint64_t rows, cols, head_width, dimension, half, position_offset;
     float scale;
+    const uint64_t* advance;  // captured step: replay offset added to position_offset
 };
 
 // Fills LDS with (cos, sin) * amplitude for this row's pairs.
 __device__ __forceinline__ void row_sincos(const RopeArgs& a, uint64_t row, float* cs, float* sn) {
-    const float position = mhip::rope_position(a.position_offset, row, a.scale);
+    const uint64_t offset = a.position_offset + (a.advance ? *a.advance : 0);
+    const float position = mhip::rope_position(offset, row, a.scale);
     for (uint64_t p = threadIdx.x; p < a.half; p += kThreads)
         mhip::rope_pair_cs(position, a.table, a.half, p, &cs[p], &sn[p]);
 }
@@ -261,7 +266,7 @@ mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t r
     mhip_status st = mhip::rope_device_table(ctx, p, &dtable);
     if (st != MHIP_OK) return st;
     RopeArgs a{in, out, dtable, rows, cols, head_width, p.dimension, half, p.position_offset,
-               p.scale};
+               p.scale, mhip::advance_ptr(ctx, MHIP_ADVANCE_POSITION_OFFSET, UINT64_MAX)};
     const unsigned lds = static_cast<unsigned>(2 * half * sizeof(float));
     const bool aligned = mhip::aligned16(in) && mhip::aligned16(out) && cols % 4 == 0 &&
                          head_width % 4 == 0;

@@ -5,6 +5,7 @@
 // :2118-2164) with the HIP runtime: the kernels are compiled ahead of time
 // for gfx950 into this library, so there is no runtime compiler step.
 #include "common.hpp"
+#include "internal.hpp"
 
 #include <cstdio>
 #include <cstring>
@@ -40,7 +41,69 @@ mhip_status check_launch(const char* what) {
     return MHIP_OK;
 }
 
+mhip_status forbid_in_capture(mhip_ctx* ctx, const char* what) {
+    if (!ctx || !ctx->capturing) return MHIP_OK;
+    const std::string reason = std::string(what) + " cannot be captured";
+    if (ctx->capture_failure.empty()) ctx->capture_failure = reason;
+    return fail(MHIP_CAPTURE_UNSUPPORTED, reason);
+}
+
+uint32_t capture_advancing(const mhip_ctx* ctx) {
+    return ctx && ctx->capturing ? ctx->advancing : 0u;
+}
+
+const uint64_t* advance_ptr(mhip_ctx* ctx, uint32_t bit, uint64_t max_offset) {
+    if (!ctx->capturing || !(ctx->advancing & bit)) return nullptr;
+    if (max_offset < ctx->max_offset) ctx->max_offset = max_offset;
+    return ctx->capture_offset;
+}
+
+// Frees `p` now, or keeps it until the last live graph is destroyed.
+static void release_buffer(mhip_ctx* ctx, void* p) {
+    if (!p) return;
+    if (ctx->live_graphs > 0) ctx->retired.push_back(p);
+    else (void)hipFree(p);
+}
+
+mhip_status workspace(mhip_ctx* ctx, size_t bytes, void** out) {
+    if (ctx->workspace_bytes < bytes) {
+        mhip_status st = forbid_in_capture(ctx, "growing the workspace");
+        if (st != MHIP_OK) return st;
+        if (ctx->workspace) {
+            (void)hipStreamSynchronize(ctx->stream);
+            release_buffer(ctx, ctx->workspace);
+            ctx->workspace = nullptr;
+            ctx->workspace_bytes = 0;
+        }
+        hipError_t err = hipMalloc(&ctx->workspace, bytes);
+        if (err != hipSuccess) {
+            ctx->workspace = nullptr;
+            return from_hip(err, "allocating the workspace");
+        }
+        ctx->workspace_bytes = bytes;
+    }
+    *out = ctx->workspace;
+    return MHIP_OK;
+}
+
 }  // namespace mhip
+
+// A captured step: the instantiated graph and the device word its advancing
+// launches read the replay offset from.
+struct mhip_graph {
+    mhip_ctx* ctx = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t* offset = nullptr;
+    uint64_t max_offset = 0;
+};
+
+namespace {
+
+__global__ void set_word_kernel(uint64_t* word, uint64_t value) { *word = value; }
+
+__global__ void clear_flags_kernel(uint32_t* flags) { flags[threadIdx.x] = 0u; }
+
+}  // namespace
 
 extern "C" {
 
@@ -107,10 +170,13 @@ mhip_status mhip_ctx_create(int ordinal, mhip_ctx** out) {
 mhip_status mhip_ctx_destroy(mhip_ctx* ctx) {
     if (!ctx) return MHIP_OK;
     (void)hipSetDevice(ctx->device);
+    mhip_capture_abort(ctx);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->flags) (void)hipFree(ctx->flags);
     for (auto& table : ctx->rope_tables) (void)hipFree(table.device);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    // Graphs not destroyed by now can no longer run: their buffers go too.
+    for (void* p : ctx->retired) (void)hipFree(p);
 
     if (ctx->timer_start) (void)hipEventDestroy(ctx->timer_start);
     if (ctx->timer_stop) (void)hipEventDestroy(ctx->timer_stop);
@@ -149,6 +215,8 @@ mhip_status mhip_alloc(mhip_ctx* ctx, size_t bytes, void** device_ptr) {
     MHIP_REQUIRE_CTX(ctx);
     if (!device_ptr) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "device_ptr is null");
     *device_ptr = nullptr;
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a device allocation"); st != MHIP_OK)
+        return st;
     (void)hipSetDevice(ctx->device);
     // A zero-byte tensor still gets a distinct, valid allocation.
     hipError_t err = hipMalloc(device_ptr, bytes ? bytes : 256);
@@ -163,12 +231,18 @@ mhip_status mhip_alloc(mhip_ctx* ctx, size_t bytes, void** device_ptr) {
 mhip_status mhip_free(mhip_ctx* ctx, void* device_ptr) {
     MHIP_REQUIRE_CTX(ctx);
     if (!device_ptr) return MHIP_OK;
+    if (ctx->capturing) {  // hipFree would wait on the capturing stream
+        ctx->deferred_frees.push_back(device_ptr);
+        return MHIP_OK;
+    }
     (void)hipSetDevice(ctx->device);
     return mhip::from_hip(hipFree(device_ptr), "freeing a device buffer");
 }
 
 mhip_status mhip_upload(mhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a host-to-device upload"); st != MHIP_OK)
+        return st;
     if (bytes == 0) return MHIP_OK;
     // Ordered after earlier kernels on the stream; waits for the copy so the
     // host buffer may be reused on return.
@@ -179,6 +253,8 @@ mhip_status mhip_upload(mhip_ctx* ctx, void* dst, const void* src, size_t bytes)
 
 mhip_status mhip_download(mhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a device-to-host download"); st != MHIP_OK)
+        return st;
     if (bytes == 0) return mhip::from_hip(hipStreamSynchronize(ctx->stream), "synchronizing");
     hipError_t err = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
@@ -194,17 +270,22 @@ mhip_status mhip_copy(mhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 mhip_status mhip_zero(mhip_ctx* ctx, void* dst, size_t bytes) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a device memset"); st != MHIP_OK) return st;
     if (bytes == 0) return MHIP_OK;
     return mhip::from_hip(hipMemsetAsync(dst, 0, bytes, ctx->stream), "zeroing a device buffer");
 }
 
 mhip_status mhip_sync(mhip_ctx* ctx) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a stream synchronization"); st != MHIP_OK)
+        return st;
     return mhip::from_hip(hipStreamSynchronize(ctx->stream), "synchronizing the stream");
 }
 
 mhip_status mhip_check_flags(mhip_ctx* ctx, uint32_t* flags_out) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "reading the failure flags"); st != MHIP_OK)
+        return st;
     uint32_t flags = 0;
     hipError_t err = hipMemcpyAsync(&flags, ctx->flags, sizeof(flags), hipMemcpyDeviceToHost,
                                     ctx->stream);
@@ -227,17 +308,141 @@ mhip_status mhip_check_flags(mhip_ctx* ctx, uint32_t* flags_out) {
 
 mhip_status mhip_timer_start(mhip_ctx* ctx) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a timer"); st != MHIP_OK) return st;
     return mhip::from_hip(hipEventRecord(ctx->timer_start, ctx->stream), "recording an event");
 }
 
 mhip_status mhip_timer_stop(mhip_ctx* ctx, float* elapsed_ms) {
     MHIP_REQUIRE_CTX(ctx);
+    if (mhip_status st = mhip::forbid_in_capture(ctx, "a timer"); st != MHIP_OK) return st;
     hipError_t err = hipEventRecord(ctx->timer_stop, ctx->stream);
     if (err == hipSuccess) err = hipEventSynchronize(ctx->timer_stop);
     float ms = 0.0f;
     if (err == hipSuccess) err = hipEventElapsedTime(&ms, ctx->timer_start, ctx->timer_stop);
     if (elapsed_ms) *elapsed_ms = ms;
     return mhip::from_hip(err, "timing the stream");
+}
+
+// ---- step capture (src/kernels.rs:1019-1349) ----
+
+mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (ctx->capturing)
+        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "a step capture is already in progress");
+    (void)hipSetDevice(ctx->device);
+    // Allocated and zeroed before the capture starts: nothing allocates while
+    // capturing.
+    uint64_t* offset = nullptr;
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&offset), 256);
+    if (err == hipSuccess) err = hipMemset(offset, 0, 256);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    if (err == hipSuccess) err = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+    if (err != hipSuccess) {
+        if (offset) (void)hipFree(offset);
+        return mhip::from_hip(err, "beginning a step capture");
+    }
+    ctx->capturing = true;
+    ctx->advancing = advancing;
+    ctx->capture_offset = offset;
+    ctx->max_offset = UINT64_MAX;
+    ctx->capture_failure.clear();
+    // The step's first work: clear the failure flags, which its launches
+    // then only ever set (a kernel, not a memset node).
+    hipLaunchKernelGGL(clear_flags_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->flags);
+    return mhip::check_launch("clearing the failure flags");
+}
+
+// Ends capture mode on the stream; returns the captured graph (or null).
+static hipGraph_t stop_capture(mhip_ctx* ctx) {
+    hipGraph_t graph = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &graph);
+    (void)hipGetLastError();
+    ctx->capturing = false;
+    for (void* p : ctx->deferred_frees) (void)hipFree(p);
+    ctx->deferred_frees.clear();
+    return graph;
+}
+
+mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offset) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (out) *out = nullptr;
+    if (!ctx->capturing) return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "no step capture is in progress");
+    hipGraph_t graph = stop_capture(ctx);
+    std::string failure = ctx->capture_failure;
+    size_t nodes = 0;
+    if (failure.empty() && !graph) failure = "the step capture met a driver error";
+    if (failure.empty() && (hipGraphGetNodes(graph, nullptr, &nodes) != hipSuccess || nodes <= 1))
+        failure = "the step capture recorded no work";
+    hipGraphExec_t exec = nullptr;
+    if (failure.empty()) {
+        hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (err != hipSuccess) failure = std::string("instantiating the step: ") + hipGetErrorString(err);
+    }
+    if (graph) (void)hipGraphDestroy(graph);
+    if (!failure.empty() || !out) {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        (void)hipFree(ctx->capture_offset);
+        ctx->capture_offset = nullptr;
+        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, failure.empty() ? "no graph handle" : failure);
+    }
+    mhip_graph* g = new mhip_graph();
+    g->ctx = ctx;
+    g->exec = exec;
+    g->offset = ctx->capture_offset;
+    g->max_offset = ctx->max_offset;
+    ctx->capture_offset = nullptr;
+    ctx->live_graphs += 1;
+    *out = g;
+    if (max_offset) *max_offset = g->max_offset;
+    return MHIP_OK;
+}
+
+mhip_status mhip_capture_abort(mhip_ctx* ctx) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (!ctx->capturing) return MHIP_OK;
+    hipGraph_t graph = stop_capture(ctx);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (ctx->capture_offset) (void)hipFree(ctx->capture_offset);
+    ctx->capture_offset = nullptr;
+    ctx->capture_failure.clear();
+    return MHIP_OK;
+}
+
+int mhip_capture_active(const mhip_ctx* ctx) { return ctx && ctx->capturing ? 1 : 0; }
+
+mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset) {
+    if (!graph) return mhip::fail(MHIP_DEVICE_UNAVAILABLE, "no captured step");
+    mhip_ctx* ctx = graph->ctx;
+    if (ctx->capturing)
+        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "a captured step cannot run while capturing");
+    if (offset > graph->max_offset)
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
+                          "offset " + std::to_string(offset) + " leaves the captured bounds (at most " +
+                              std::to_string(graph->max_offset) + ")");
+    // The offset is written by a kernel on the same stream, ahead of the graph.
+    hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
+    mhip_status st = mhip::check_launch("writing the replay offset");
+    if (st != MHIP_OK) return st;
+    return mhip::from_hip(hipGraphLaunch(graph->exec, ctx->stream), "launching a captured step");
+}
+
+uint64_t mhip_graph_max_offset(const mhip_graph* graph) { return graph ? graph->max_offset : 0; }
+
+mhip_status mhip_graph_destroy(mhip_graph* graph) {
+    if (!graph) return MHIP_OK;
+    mhip_ctx* ctx = graph->ctx;
+    if (ctx->capturing)
+        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "a captured step cannot be released while capturing");
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipFree(graph->offset);
+    ctx->live_graphs -= 1;
+    if (ctx->live_graphs == 0) {
+        for (void* p : ctx->retired) (void)hipFree(p);
+        ctx->retired.clear();
+    }
+    delete graph;
+    return MHIP_OK;
 }
 
 }  // extern "C"

@@ -91,6 +91,7 @@ class AttentionParams(ctypes.Structure):
         ("kv_batch_stride", ctypes.c_uint64),
         ("v_batch_stride", ctypes.c_uint64),
         ("out_batch_stride", ctypes.c_uint64),
+        ("bounded_key_count", ctypes.c_uint32),
     ]
 
 
@@ -138,6 +139,13 @@ SIGNATURES = {
     "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
     "mhip_attention_f32": [_CTX, _P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
     "mhip_kv_write_f32": [_CTX, _P, _U64, _U64, _P, _U64, _U64],
+    "mhip_capture_begin": [_CTX, ctypes.c_uint32],
+    "mhip_capture_end": [_CTX, ctypes.POINTER(_P), ctypes.POINTER(_U64)],
+    "mhip_capture_abort": [_CTX],
+    "mhip_graph_launch": [_P, _U64],
+    "mhip_graph_destroy": [_P],
+    "mhip_capture_active": [_CTX],
+    "mhip_graph_max_offset": [_P],
 }
 
 _RESTYPES = {
@@ -145,6 +153,7 @@ _RESTYPES = {
     "mhip_status_name": ctypes.c_char_p,
     "mhip_version": ctypes.c_char_p,
     "mhip_rope_params_default": None,
+    "mhip_graph_max_offset": _U64,
 }
 
 _lib = None

@@ -115,6 +115,16 @@ class Device:
                  host.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
         return arr
 
+    def write(self, arr: DeviceArray, host: np.ndarray) -> DeviceArray:
+        """Copies `host` into the existing buffer `arr` (same byte size)."""
+        host = np.ascontiguousarray(host, dtype=arr.dtype)
+        if host.nbytes != arr.nbytes:
+            raise ValueError(f"write of {host.nbytes} bytes into a {arr.nbytes}-byte buffer")
+        if arr.nbytes:
+            call("mhip_upload", self.ctx, ctypes.c_void_p(arr.ptr),
+                 host.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
+        return arr
+
     def download(self, arr: DeviceArray) -> np.ndarray:
         out = np.empty(arr.shape, dtype=arr.dtype)
         call("mhip_download", self.ctx, out.ctypes.data_as(ctypes.c_void_p),
@@ -138,4 +148,47 @@ class Device:
         return ms.value
 
 
-__all__ = ["Device", "DeviceArray", "MagnetarHipError", "device_count"]
+    # ---- step capture (mhip_capture_*) ----
+    def capture_begin(self, advancing: int = 0) -> None:
+        """Records the following launches into a graph instead of running them;
+        `advancing` is a mask of ADVANCE_* attributes a replay offset moves."""
+        call("mhip_capture_begin", self.ctx, advancing)
+
+    def capture_end(self) -> "CapturedStep":
+        handle = ctypes.c_void_p()
+        bound = ctypes.c_uint64(0)
+        call("mhip_capture_end", self.ctx, ctypes.byref(handle), ctypes.byref(bound))
+        return CapturedStep(self, handle, bound.value)
+
+    def capture_abort(self) -> None:
+        call("mhip_capture_abort", self.ctx)
+
+
+ADVANCE_POSITION_OFFSET, ADVANCE_KEY_COUNT, ADVANCE_ROW_OFFSET = 1, 2, 4
+
+
+class CapturedStep:
+    """A captured launch sequence (HIP graph); launch(offset) replays it with
+    every advancing attribute increased by `offset` (at most `max_offset`)."""
+
+    def __init__(self, device: Device, handle, max_offset: int):
+        self.device, self._h, self.max_offset = device, handle, max_offset
+
+    def launch(self, offset: int = 0) -> None:
+        call("mhip_graph_launch", self._h, offset)
+
+    def close(self) -> None:
+        # A closed device took its graphs' memory with it.
+        if self._h and self.device.ctx:
+            lib().mhip_graph_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+__all__ = ["Device", "DeviceArray", "CapturedStep", "MagnetarHipError", "device_count",
+           "ADVANCE_POSITION_OFFSET", "ADVANCE_KEY_COUNT", "ADVANCE_ROW_OFFSET"]

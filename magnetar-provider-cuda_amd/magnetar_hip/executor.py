@@ -31,6 +31,7 @@ KERNEL_ERRORS = {
     7: "KernelAttributeUnsupported",
     8: "KernelNotFound",
     9: "KernelTimeout",
+    10: "StepReplayInvalidated",
 }
 HEALTH = {0: "Available", 1: "Degraded", 2: "Unavailable"}
 OBSERVATIONS = {0: "KernelDispatchStarted", 1: "KernelDispatchCompleted",
@@ -98,6 +99,12 @@ _SIGS = {
     "mhip_executor_write_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t], ctypes.c_int),
     "mhip_executor_write_tensor_values": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
     "mhip_executor_write_zeroed_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int], ctypes.c_int),
+    "mhip_executor_supports_step_capture": ([_P], ctypes.c_int),
+    "mhip_executor_begin_step_capture": ([_P, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int], ctypes.c_int),
+    "mhip_executor_end_step_capture": ([_P, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_int),
+    "mhip_executor_abort_step_capture": ([_P], ctypes.c_int),
+    "mhip_executor_replay_step": ([_P, ctypes.c_char_p, _U64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_P), ctypes.POINTER(_U64), ctypes.c_int], ctypes.c_int),
+    "mhip_executor_release_step_capture": ([_P, ctypes.c_char_p], ctypes.c_int),
     "mhip_executor_write_zeroed_kv_store": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _U64, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "mhip_executor_read_tensor": ([_P, ctypes.c_char_p, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "mhip_executor_read_tensor_values": ([_P, ctypes.c_char_p, _P, ctypes.c_size_t], ctypes.c_int),
@@ -341,6 +348,39 @@ class Executor:
 
     def execute(self, inv: KernelInvocation) -> None:
         self.complete_kernel(self.submit_kernel(inv))
+
+    # ---- step capture (src/executor.rs:177-336) ----
+    def supports_step_capture(self) -> bool:
+        return bool(_lib_bound().mhip_executor_supports_step_capture(self._h))
+
+    def begin_step_capture(self, advancing_attributes: Sequence[str] = ()) -> None:
+        names = (ctypes.c_char_p * max(1, len(advancing_attributes)))(
+            *[a.encode() for a in advancing_attributes])
+        _check(_lib_bound().mhip_executor_begin_step_capture(self._h, names,
+                                                             len(advancing_attributes)))
+
+    def end_step_capture(self) -> str:
+        """Instantiates the captured step and runs it once; returns its id."""
+        buf = ctypes.create_string_buffer(256)
+        _check(_lib_bound().mhip_executor_end_step_capture(self._h, buf, 256))
+        return buf.value.decode()
+
+    def abort_step_capture(self) -> None:
+        _check(_lib_bound().mhip_executor_abort_step_capture(self._h))
+
+    def replay_step(self, capture_id: str, offset: int = 0, inputs=None) -> None:
+        """Writes `inputs` ({resource id: f32 array}) into the step's buffers and
+        runs it with every advancing attribute increased by `offset`."""
+        items = [(k, np.ascontiguousarray(v, np.float32).ravel()) for k, v in (inputs or {}).items()]
+        n = len(items)
+        ids = (ctypes.c_char_p * max(1, n))(*[k.encode() for k, _ in items])
+        ptrs = (_P * max(1, n))(*[a.ctypes.data for _, a in items])
+        lens = (_U64 * max(1, n))(*[a.size for _, a in items])
+        _check(_lib_bound().mhip_executor_replay_step(self._h, capture_id.encode(), offset, ids,
+                                                      ptrs, lens, n))
+
+    def release_step_capture(self, capture_id: str) -> None:
+        _check(_lib_bound().mhip_executor_release_step_capture(self._h, capture_id.encode()))
 
     def set_sync_nodes(self, enabled: bool) -> None:
         _lib.check(_lib_bound().mhip_executor_set_sync_nodes(self._h, int(enabled)))

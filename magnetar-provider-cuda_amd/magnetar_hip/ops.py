@@ -152,6 +152,7 @@ def attention_params(seq_len, kv_rows, head_count, head_dimension, kv_head_count
     p.window_size = -1 if window_size is None else window_size
     p.scale = 0.0 if scale is None else scale
     p.batch = batch
+    p.bounded_key_count = int(key_count is not None)
     return p
 
 

@@ -1,0 +1,266 @@
+"""GPU: step capture and replay (reference src/executor.rs:177-336,
+src/kernels.rs:1019-1349; tests src/tests_hardware_hot_path.rs:633-833).
+
+A captured step is a HIP graph of the context's stream. Replays with an
+offset move every advancing attribute (RoPE position_offset, attention
+key_count, kv-write row_offset) by it, and must equal the same invocations
+dispatched eagerly at the advanced values, bit for bit. Each graph is replayed
+several times with eager work and synchronisation in between, and every replay
+is checked.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def provider():
+    import magnetar_hip
+    p = magnetar_hip.Provider()
+    yield p
+    p.close()
+
+
+@pytest.fixture()
+def ex(provider):
+    return provider.execution_api()
+
+
+def inv(kernel, inputs, output, attrs=None):
+    from magnetar_hip import KernelInvocation, TensorRef
+    return KernelInvocation(kernel, [TensorRef(i) for i in inputs], [TensorRef(output)], attrs or {})
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def test_the_executor_supports_step_capture(ex):
+    assert ex.supports_step_capture()
+
+
+def test_a_captured_step_replays_with_an_advanced_position(ex):
+    """src/tests_hardware_hot_path.rs:633-727: rope then rmsnorm, captured at
+    position 3 and replayed at offset 4 with other inputs, equals the eager
+    step at position 7."""
+    from magnetar_hip import Integer, KernelError
+    first = np.array([[0.5, -1.0, 2.0, 0.25], [1.5, 3.0, -0.75, 1.0]], np.float32)
+    second = np.array([[-2.0, 0.5, 1.0, 4.0], [0.0, -1.5, 2.5, 0.75]], np.float32)
+    ex.write_tensor("replay.norm.weight", np.array([0.5, 1.0, 1.5, 2.0], np.float32))
+
+    def step(position, read=True):
+        ex.execute(inv("rope", ["replay.x"], "replay.rope.out",
+                       {"base": 10000.0, "dimension": 4, "position_offset": Integer(position)}))
+        ex.execute(inv("rmsnorm", ["replay.rope.out", "replay.norm.weight"], "replay.sum.out",
+                       {"epsilon": 1e-6}))
+        return ex.read_tensor("replay.sum.out") if read else None
+
+    ex.write_tensor("replay.x", second)
+    second_at_7 = step(7)
+    ex.write_tensor("replay.x", first)
+    first_at_3 = step(3)
+    assert not np.array_equal(first_at_3, second_at_7)
+
+    ex.begin_step_capture(["position_offset"])
+    step(3, read=False)
+    capture = ex.end_step_capture()
+    assert capture.endswith(":step-capture:" + capture.rsplit(":", 1)[1])
+    assert np.array_equal(bits(ex.read_tensor("replay.sum.out")), bits(first_at_3))
+    for _ in range(3):
+        ex.replay_step(capture, 4, {"replay.x": second})
+        assert np.array_equal(bits(ex.read_tensor("replay.sum.out")), bits(second_at_7))
+        ex.replay_step(capture, 0, {"replay.x": first})
+        assert np.array_equal(bits(ex.read_tensor("replay.sum.out")), bits(first_at_3))
+
+    # A fresh upload gives the input another buffer.
+    ex.write_tensor("replay.x", first)
+    with pytest.raises(KernelError) as err:
+        ex.replay_step(capture, 0, {"replay.x": first})
+    assert err.value.code == "StepReplayInvalidated"
+    ex.release_step_capture(capture)
+    with pytest.raises(KernelError) as err:
+        ex.replay_step(capture, 0, {})
+    assert err.value.code == "StepReplayInvalidated"
+
+    # A host upload cannot be captured: the capture fails, the stream works.
+    ex.begin_step_capture(["position_offset"])
+    with pytest.raises(KernelError):
+        ex.write_tensor("replay.x", first)
+    with pytest.raises(KernelError) as err:
+        ex.end_step_capture()
+    assert "cannot be captured" in err.value.detail
+    assert np.array_equal(bits(step(3)), bits(first_at_3))
+
+
+def test_capture_refuses_what_it_cannot_replay(ex):
+    from magnetar_hip import KernelError
+    ex.write_tensor("cap.a", np.ones((2, 8), np.float32))
+    ex.execute(inv("softmax", ["cap.a"], "cap.s"))
+    ex.begin_step_capture([])
+    with pytest.raises(KernelError):
+        ex.begin_step_capture([])          # one capture at a time
+    with pytest.raises(KernelError):
+        ex.execute(inv("softmax", ["cap.a"], "cap.s"))
+    with pytest.raises(KernelError) as err:
+        ex.end_step_capture()
+    assert "softmax cannot be captured" in err.value.detail
+    # A fresh output needs an allocation, which cannot be captured either.
+    ex.begin_step_capture([])
+    with pytest.raises(KernelError):
+        ex.execute(inv("silu", ["cap.a"], "cap.new_output"))
+    ex.abort_step_capture()
+    with pytest.raises(KernelError):
+        ex.end_step_capture()               # nothing in progress
+    ex.execute(inv("silu", ["cap.a"], "cap.new_output"))
+    assert ex.read_tensor("cap.new_output").shape == (2, 8)
+
+
+def _values(count, seed):
+    """The reference test's generator (src/tests_hardware_hot_path.rs:752-756)."""
+    i = np.arange(count, dtype=np.int64)
+    return ((((i * 37 + seed * 11) % 97).astype(np.float32) - 48.0) / 64.0).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,head_dimension", [(16, 64), (32, 128), (8, 64)])
+def test_a_captured_prefill_attention_replays_at_its_key_count(ex, rows, head_dimension):
+    """src/tests_hardware_hot_path.rs:729-827: several query rows replay with new
+    queries exactly like an eager dispatch, and only at offset 0."""
+    from magnetar_hip import Integer, KernelError
+    width = 2 * head_dimension
+    capacity = 4 * rows
+    pre = f"prefill-attention.{rows}.{head_dimension}"
+    first = _values(rows * width, 1).reshape(rows, width)
+    second = _values(rows * width, 2).reshape(rows, width)
+    ex.write_tensor(pre + ".k", _values(capacity * width, 3).reshape(capacity, width))
+    ex.write_tensor(pre + ".v", _values(capacity * width, 4).reshape(capacity, width))
+    attrs = {"head_count": Integer(2), "head_dimension": Integer(head_dimension), "causal": True,
+             "key_count": Integer(rows)}
+
+    def attention():
+        ex.execute(inv("attention", [pre + ".q", pre + ".k", pre + ".v"], pre + ".out", attrs))
+
+    ex.write_tensor(pre + ".q", second)
+    attention()
+    expected_second = ex.read_tensor(pre + ".out")
+    ex.write_tensor(pre + ".q", first)
+    attention()
+    expected_first = ex.read_tensor(pre + ".out")
+    assert not np.array_equal(expected_first, expected_second)
+
+    ex.begin_step_capture(["key_count"])
+    attention()
+    capture = ex.end_step_capture()
+    assert np.array_equal(bits(ex.read_tensor(pre + ".out")), bits(expected_first))
+    for _ in range(2):
+        ex.replay_step(capture, 0, {pre + ".q": second})
+        assert np.array_equal(bits(ex.read_tensor(pre + ".out")), bits(expected_second))
+        ex.replay_step(capture, 0, {pre + ".q": first})
+        assert np.array_equal(bits(ex.read_tensor(pre + ".out")), bits(expected_first))
+    with pytest.raises(KernelError) as err:
+        ex.replay_step(capture, 1, {pre + ".q": first})
+    assert err.value.code == "StepReplayInvalidated"
+    ex.release_step_capture(capture)
+
+
+@pytest.mark.parametrize("heads,kv_heads,dim", [(4, 4, 64), (8, 2, 128), (2, 1, 4)])
+def test_a_captured_decode_step_advances_position_cache_row_and_key_count(ex, orc, heads,
+                                                                          kv_heads, dim):
+    """A decode step -- RoPE on q and k at position p, kv-write of k and v at row
+    p, attention over key_count p + 1 -- captured at p = 0 and replayed at
+    offset t equals the eager step at p = t, outputs and cache rows."""
+    from magnetar_hip import Integer
+    steps, capacity = 6, 40
+    qw, kw = heads * dim, kv_heads * dim
+    pre = f"dec.{heads}.{kv_heads}.{dim}"
+    q_in = [orc.normal(qw, 10 + t).reshape(1, qw) for t in range(steps)]
+    k_in = [orc.normal(kw, 30 + t).reshape(1, kw) for t in range(steps)]
+    v_in = [orc.normal(kw, 50 + t).reshape(1, kw) for t in range(steps)]
+
+    def step(t, read=True):
+        rope = {"dimension": Integer(dim), "position_offset": Integer(t)}
+        ex.execute(inv("rope", [pre + ".q"], pre + ".qr", dict(rope, head_count=Integer(heads))))
+        ex.execute(inv("rope", [pre + ".k"], pre + ".kr", dict(rope, head_count=Integer(kv_heads))))
+        ex.execute(inv("kv-write", [pre + ".kc", pre + ".kr"], pre + ".kc", {"row_offset": Integer(t)}))
+        ex.execute(inv("kv-write", [pre + ".vc", pre + ".v"], pre + ".vc", {"row_offset": Integer(t)}))
+        ex.execute(inv("attention", [pre + ".qr", pre + ".kc", pre + ".vc"], pre + ".out",
+                       {"head_count": Integer(heads), "head_dimension": Integer(dim),
+                        "kv_head_count": Integer(kv_heads), "causal": True,
+                        "key_count": Integer(t + 1)}))
+        if read:
+            return ex.read_tensor(pre + ".out"), ex.read_tensor(pre + ".kc"), ex.read_tensor(pre + ".vc")
+
+    # Eager reference.
+    assert ex.write_zeroed_kv_store(pre + ".kc", (capacity, kw))
+    assert ex.write_zeroed_kv_store(pre + ".vc", (capacity, kw))
+    eager = []
+    for t in range(steps):
+        ex.write_tensor(pre + ".q", q_in[t])
+        ex.write_tensor(pre + ".k", k_in[t])
+        ex.write_tensor(pre + ".v", v_in[t])
+        eager.append(step(t))
+
+    # Fresh caches; one eager step creates the outputs, then capture at p = 0.
+    assert ex.write_zeroed_kv_store(pre + ".kc", (capacity, kw))
+    assert ex.write_zeroed_kv_store(pre + ".vc", (capacity, kw))
+    ex.write_tensor(pre + ".q", q_in[0])
+    ex.write_tensor(pre + ".k", k_in[0])
+    ex.write_tensor(pre + ".v", v_in[0])
+    step(0)
+    ex.begin_step_capture(["position_offset", "row_offset", "key_count"])
+    step(0, read=False)
+    capture = ex.end_step_capture()
+    for t in range(steps):
+        if t:
+            ex.replay_step(capture, t, {pre + ".q": q_in[t], pre + ".k": k_in[t], pre + ".v": v_in[t]})
+        out, kc, vc = (ex.read_tensor(pre + s) for s in (".out", ".kc", ".vc"))
+        assert np.array_equal(bits(out), bits(eager[t][0])), t
+        assert np.array_equal(bits(kc), bits(eager[t][1])), t
+        assert np.array_equal(bits(vc), bits(eager[t][2])), t
+    ex.release_step_capture(capture)
+
+
+def test_a_captured_decoder_block_replays_decode_steps(dev, orc):
+    """mhip_block_forward captured once at position P (all three attributes
+    advancing) and replayed at offset t equals the eager block at P + t."""
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from magnetar_hip.device import (ADVANCE_KEY_COUNT, ADVANCE_POSITION_OFFSET,
+                                     ADVANCE_ROW_OFFSET)
+    s = Shapes(vocab=512, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024)
+    w = {}
+    for i, (name, shape) in enumerate(s.weight_shapes().items()):
+        n = int(np.prod(shape))
+        w[name] = (orc.normal(n, 700 + i, 1.0, 0.1) if name.endswith("norm")
+                   else orc.normal(n, 700 + i, 0.0, 0.02)).reshape(shape)
+    rows, P, steps = 48, 20, 5
+    history_k = orc.normal(rows * 128, 790, 0.0, 0.5).reshape(rows, 128)
+    history_v = orc.normal(rows * 128, 791, 0.0, 0.5).reshape(rows, 128)
+    ids = [orc.token_ids(1, 800 + t, 512) for t in range(steps)]
+
+    eager_block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1)
+    eager_block.k_cache, eager_block.v_cache = dev.upload(history_k), dev.upload(history_v)
+    eager = []
+    for t in range(steps):
+        out = eager_block.forward(dev.upload(ids[t]), P + t).numpy()
+        eager.append((out, eager_block.k_cache.numpy(), eager_block.v_cache.numpy()))
+
+    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1)
+    block.k_cache, block.v_cache = dev.upload(history_k), dev.upload(history_v)
+    ids_buf = dev.upload(ids[0])
+    out = dev.empty((1, s.hidden))
+    block.forward(ids_buf, P, out)  # sizes scratch and caches the RoPE table
+    dev.capture_begin(ADVANCE_POSITION_OFFSET | ADVANCE_KEY_COUNT | ADVANCE_ROW_OFFSET)
+    block.forward(ids_buf, P, out)
+    graph = dev.capture_end()
+    assert graph.max_offset == rows - (P + 1)
+    for t in range(steps):
+        dev.write(ids_buf, ids[t])
+        graph.launch(t)
+        assert np.array_equal(bits(out.numpy()), bits(eager[t][0])), t
+        assert np.array_equal(bits(block.k_cache.numpy()), bits(eager[t][1])), t
+        assert np.array_equal(bits(block.v_cache.numpy()), bits(eager[t][2])), t
+    import magnetar_hip
+    with pytest.raises(magnetar_hip.MagnetarHipError):
+        graph.launch(rows - P)  # past the cache
+    dev.check_flags()
+    graph.close()
