@@ -227,6 +227,13 @@ def decoder_cases(dev, orc):
     w0 = 4 * (4 * 256 * 256 + 3 * 256 * 688)
     cases.append(Case("decoder_c1_seq32", lambda i: b0.forward(ids0, 0, out0), w0, "hbm",
                       [32, 256], tokens=32))
+    # The same block captured once as a HIP graph and replayed (launch-bound).
+    b0.forward(ids0, 0, out0)
+    dev.capture_begin(0)
+    b0.forward(ids0, 0, out0)
+    g0 = dev.capture_end()
+    cases.append(Case("decoder_c1_seq32_graph", lambda i: g0.launch(0), w0, "hbm", [32, 256],
+                      tokens=32))
     big = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     b4 = block(big, 4, 2049, 512)
     ids_p = dev.upload(orc.token_ids(512, seed(4, 8), 32000))
@@ -239,6 +246,15 @@ def decoder_cases(dev, orc):
     weight_bytes = 4 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
     kv_bytes = 2 * 2049 * 4096 * 4
     cases.append(Case("decoder_c5_decode_kv2048", lambda i: b4.forward(ids_d, 2048, out_d),
+                      weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
+    # A decode step captured with position, cache row and key count advancing
+    # (here at the last cache row, so replays run at offset 0).
+    from magnetar_hip.device import ADVANCE_KEY_COUNT, ADVANCE_POSITION_OFFSET, ADVANCE_ROW_OFFSET
+    b4.forward(ids_d, 2048, out_d)
+    dev.capture_begin(ADVANCE_POSITION_OFFSET | ADVANCE_KEY_COUNT | ADVANCE_ROW_OFFSET)
+    b4.forward(ids_d, 2048, out_d)
+    g4 = dev.capture_end()
+    cases.append(Case("decoder_c5_decode_kv2048_graph", lambda i: g4.launch(0),
                       weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
     return cases
 
