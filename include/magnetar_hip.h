@@ -218,6 +218,28 @@ typedef struct {
 mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
                                float* out, const mhip_attention_params* params);
 
+/* Compact bf16 weights (execute-native-half-precision, src/kernels.rs:1665-1723):
+ * the matmul with b given as bf16 bit patterns ([k, n], or [n, k] when
+ * transpose_b) and the embedding lookup with a bf16 table. Each widens the
+ * weight exactly (a bf16 value is an f32 with zero low bits) and computes in
+ * f32, so the result equals mhip_matmul_f32 / mhip_embedding_f32 on the
+ * widened weight bit for bit, reading half the weight bytes. */
+mhip_status mhip_matmul_bf16w_f32(mhip_ctx* ctx, const float* a, const uint16_t* b, float* out,
+                                  uint64_t m, uint64_t k, uint64_t n, int transpose_a,
+                                  int transpose_b, const float* addend, int addend_mode);
+mhip_status mhip_embedding_bf16w_f32(mhip_ctx* ctx, const uint16_t* table, uint64_t vocab,
+                                     uint64_t dim, const float* ids, uint64_t num_ids, float* out);
+
+/* Greedy next-token selection (src/kernels.rs:4437-4488): the column of
+ * logits row `row` ([rows, cols]) with the largest score / temperature (score
+ * as is when temperature is 0) among finite scores outside the `range_count`
+ * excluded [start, end) pairs in `excluded` (host memory, 2 * range_count
+ * values); ties go to the lowest column. *column = -1 when no column is
+ * eligible. Downloads 8 bytes. */
+mhip_status mhip_greedy_select_f32(mhip_ctx* ctx, const float* logits, uint64_t rows,
+                                   uint64_t cols, uint64_t row, const uint64_t* excluded,
+                                   uint32_t range_count, float temperature, int64_t* column);
+
 /* kv-write (src/kernels.rs:2270-2325): store [capacity, width] rows
  * [row_offset, row_offset + count) = rows [count, width], in place; other rows
  * unchanged. An overrun is ShapeUnsupported and writes nothing. */
@@ -255,6 +277,10 @@ uint64_t mhip_graph_max_offset(const mhip_graph* graph);
 mhip_status mhip_graph_destroy(mhip_graph* graph);
 
 /* ---- decoder block, chained device-resident (src/tests_hardware_hot_path.rs:339-526) ---- */
+/* Block weight storage: f32, or compact bf16 bit patterns for the matrices
+ * (embedding, wq, wk, wv, wo, w_gate, w_up, w_down; norms stay f32). */
+typedef enum { MHIP_WEIGHTS_F32 = 0, MHIP_WEIGHTS_BF16 = 1 } mhip_weight_format;
+
 typedef struct {
     uint64_t hidden;            /* = heads * head_dim */
     uint64_t heads;
@@ -264,11 +290,14 @@ typedef struct {
     uint64_t vocab;
     float eps;                  /* RMSNorm epsilon */
     float rope_base;            /* RoPE theta */
+    uint32_t weight_format;     /* mhip_weight_format */
 } mhip_block_config;
 
-/* Device pointers, all f32 row-major: embedding [vocab, hidden]; attn_norm and
+/* Device pointers, row-major: embedding [vocab, hidden]; attn_norm and
  * ffn_norm [hidden]; wq [hidden, H*hd], wk and wv [hidden, Hkv*hd],
- * wo [H*hd, hidden]; w_gate and w_up [hidden, ffn]; w_down [ffn, hidden]. */
+ * wo [H*hd, hidden]; w_gate and w_up [hidden, ffn]; w_down [ffn, hidden].
+ * f32, except that the matrices hold bf16 bit patterns (2 bytes each, the
+ * pointer reinterpreted) under MHIP_WEIGHTS_BF16. */
 typedef struct {
     const float* embedding;
     const float* attn_norm;
@@ -396,6 +425,16 @@ mhip_kernel_error mhip_executor_write_tensor_values(mhip_executor* ex, const cha
                                                     const float* values);
 mhip_kernel_error mhip_executor_write_zeroed_tensor(mhip_executor* ex, const char* id,
                                                     const uint64_t* shape, int rank, int dtype);
+/* write_weight_tensor (src/executor.rs:384-399, src/kernels.rs:1665-1723):
+ * `values` (f32) stored compact as bf16 bit patterns when the tensor is a
+ * matrix of at least 65536 values that are all exact bf16 values (*compact =
+ * 1), else as f32. Lossless either way: reads return the same f32 values.
+ * Kernels read compact weights directly where the reference does (matmul,
+ * matmul-bias, matmul-residual: b; gated-matmul: gate, up; embedding:
+ * table); any other use stores the weight as f32 first, for good. */
+mhip_kernel_error mhip_executor_write_weight_tensor(mhip_executor* ex, const char* id,
+                                                    const uint64_t* shape, int rank,
+                                                    const float* values, int* compact);
 /* KV store precisions (KvStorePrecision: F32, Tq4, Tq3). */
 typedef enum { MHIP_KV_F32 = 0, MHIP_KV_TQ4 = 1, MHIP_KV_TQ3 = 2 } mhip_kv_precision;
 /* write_zeroed_kv_store (src/executor.rs:560-602): a zeroed f32 store of
@@ -432,6 +471,13 @@ mhip_kernel_error mhip_executor_complete_kernel(mhip_executor* ex, uint64_t hand
 /* submit + complete in one call. */
 mhip_kernel_error mhip_executor_execute(mhip_executor* ex, const mhip_invocation* inv);
 /* MAGNETAR_HIP_SYNC_NODES equivalent: wait for the device after each dispatch. */
+/* select_greedy_column (src/executor.rs:2549-2564): greedy selection on the
+ * stored logits resource; *column = -1 when none is eligible. */
+mhip_kernel_error mhip_executor_select_greedy_column(mhip_executor* ex, const char* logits,
+                                                     uint64_t row, const uint64_t* excluded,
+                                                     uint32_t range_count, float temperature,
+                                                     int64_t* column);
+
 /* Step capture (src/executor.rs:177-336): the invocations between begin and
  * end are recorded into a HIP graph (see mhip_capture_begin); `advancing`
  * names the attributes a replay offset increases ("position_offset",

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -72,6 +73,31 @@ __device__ __forceinline__ float4 load_nt(const float4* p) {
 __device__ __forceinline__ uint4 load_nt(const uint4* p) {
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+// Operand elements: f32, or bf16 bit patterns (compact weights) widened to
+// f32 exactly -- a bf16 value is the f32 whose low 16 bits are zero.
+__device__ __forceinline__ float elem(const float* p) { return *p; }
+__device__ __forceinline__ float elem(const uint16_t* p) {
+    return __uint_as_float(static_cast<uint32_t>(*p) << 16);
+}
+__device__ __forceinline__ float4 widen(uint2 u) {
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u));
+}
+// Four consecutive elements (16-byte aligned f32, 8-byte aligned bf16).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t* p) {
+    return widen(*reinterpret_cast<const uint2*>(p));
+}
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+// The same, read once (streamed): non-temporal.
+__device__ __forceinline__ float4 load4_nt(const float* p) {
+    return load_nt(reinterpret_cast<const float4*>(p));
+}
+__device__ __forceinline__ float4 load4_nt(const uint16_t* p) {
+    const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return widen(make_uint2(t.x, t.y));
 }
 
 // silu(v) = v * (1 / (1 + e^-v)) (src/kernels.cu:73-79).

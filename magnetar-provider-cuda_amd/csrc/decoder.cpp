@@ -78,6 +78,16 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     const uint64_t kv_dim = c.kv_heads * c.head_dim;
     float* k_rows = k_cache + position * kv_dim;
     float* v_rows = v_cache + position * kv_dim;
+    if (c.weight_format != MHIP_WEIGHTS_F32 && c.weight_format != MHIP_WEIGHTS_BF16)
+        return MHIP_DTYPE_UNSUPPORTED;
+    const bool bf16 = c.weight_format == MHIP_WEIGHTS_BF16;
+    // A weight matrix product, f32 or compact bf16 weights.
+    auto mm = [&](const float* lhs, const float* weight, float* dst, uint64_t m, uint64_t k,
+                  uint64_t n, const float* addend, int mode) {
+        return bf16 ? mhip_matmul_bf16w_f32(ctx, lhs, reinterpret_cast<const uint16_t*>(weight),
+                                            dst, m, k, n, 0, 0, addend, mode)
+                    : mhip_matmul_f32(ctx, lhs, weight, dst, m, k, n, 0, 0, addend, mode);
+    };
     mhip_status st;
 #define MHIP_TRY(call)                 \
     do {                               \
@@ -86,9 +96,11 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     } while (0)
     // Embedding + RMSNorm in one pass where the row fits the fused kernel.
     st = mhip::embed_rmsnorm_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, w->attn_norm,
-                                 c.eps, x, h);
+                                 c.eps, x, h, bf16);
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
-        MHIP_TRY(mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
+        MHIP_TRY(bf16 ? mhip_embedding_bf16w_f32(ctx, reinterpret_cast<const uint16_t*>(w->embedding),
+                                                 c.vocab, c.hidden, ids, seq, x)
+                      : mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
         MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
     } else if (st != MHIP_OK) {
         return st;
@@ -107,14 +119,14 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     mhip::GemvTarget qkv[3] = {{w->wq, c.heads * c.head_dim, q},
                                {w->wk, kv_dim, k_rows, true, rows_left},
                                {w->wv, kv_dim, v_rows, true, rows_left}};
-    st = mhip::gemv_set_f32(ctx, h, seq, c.hidden, qkv, 3, mhip::kGemvRopeQK, rope);
+    st = mhip::gemv_set_f32(ctx, h, seq, c.hidden, qkv, 3, mhip::kGemvRopeQK, rope, bf16);
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
         // The separate matmuls write fixed rows of the cache.
         if (mhip::capture_advancing(ctx) & MHIP_ADVANCE_ROW_OFFSET)
             return mhip::forbid_in_capture(ctx, "a K/V append of more than 8 rows with an advancing row offset");
-        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, 0, 0, nullptr, 0));
-        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wk, k_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
-        MHIP_TRY(mhip_matmul_f32(ctx, h, w->wv, v_rows, seq, c.hidden, kv_dim, 0, 0, nullptr, 0));
+        MHIP_TRY(mm(h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, nullptr, 0));
+        MHIP_TRY(mm(h, w->wk, k_rows, seq, c.hidden, kv_dim, nullptr, 0));
+        MHIP_TRY(mm(h, w->wv, v_rows, seq, c.hidden, kv_dim, nullptr, 0));
         MHIP_TRY(mhip_rope_f32(ctx, q, q, seq, c.heads * c.head_dim, &rope[0]));
         MHIP_TRY(mhip_rope_f32(ctx, k_rows, k_rows, seq, kv_dim, &rope[1]));
     } else if (st != MHIP_OK) {
@@ -134,20 +146,20 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     ap.window_size = -1;
     ap.batch = 1;
     MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
-    MHIP_TRY(mhip_matmul_f32(ctx, a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, 0, 0, x, 2));
+    MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
     MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
     // Decode: gate and up as one set of GEMVs whose reduction writes
     // silu(gate) * up. Otherwise two matmuls and silu-mul.
     const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};
-    st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr);
+    st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr, bf16);
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
-        MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_gate, g, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
-        MHIP_TRY(mhip_matmul_f32(ctx, h2, w->w_up, u, seq, c.hidden, c.ffn, 0, 0, nullptr, 0));
+        MHIP_TRY(mm(h2, w->w_gate, g, seq, c.hidden, c.ffn, nullptr, 0));
+        MHIP_TRY(mm(h2, w->w_up, u, seq, c.hidden, c.ffn, nullptr, 0));
         MHIP_TRY(mhip_silu_mul_f32(ctx, g, u, g, seq * c.ffn));
     } else if (st != MHIP_OK) {
         return st;
     }
-    MHIP_TRY(mhip_matmul_f32(ctx, g, w->w_down, out, seq, c.ffn, c.hidden, 0, 0, x2, 2));
+    MHIP_TRY(mm(g, w->w_down, out, seq, c.ffn, c.hidden, x2, 2));
 #undef MHIP_TRY
     return MHIP_OK;
 }

@@ -95,6 +95,9 @@ struct Buffer {
     size_t bytes = 0;
     Shape shape;
     int dtype = MHIP_DTYPE_F32;
+    // An f32 weight stored compact as bf16 bit patterns (write_weight_tensor,
+    // src/kernels.rs:1665-1723): 2 bytes per value, widened exactly on read.
+    bool compact = false;
 
     Buffer(mhip_ctx* c, size_t nbytes, Shape s, int dt) : ctx(c), bytes(nbytes), shape(std::move(s)), dtype(dt) {
         check(mhip_alloc(ctx, bytes, &ptr));
@@ -243,7 +246,7 @@ struct mhip_executor {
     // (`alloc_output`, src/kernels.rs:2342-2355), else a fresh one.
     BufferPtr alloc_output(BufferPtr& offered, const Shape& shape, int dtype) {
         const size_t bytes = numel(shape) * dtype_size(dtype);
-        if (offered && offered->bytes == bytes) {
+        if (offered && offered->bytes == bytes && !offered->compact) {
             BufferPtr out = std::move(offered);
             out->shape = shape;
             out->dtype = dtype;
@@ -330,7 +333,9 @@ struct mhip_executor {
         const std::optional<float> factor = attr_float_opt(inv, "scale");
         const uint64_t num = numel(ids.shape);
         BufferPtr out = alloc_output(offered, Shape{num, dim}, MHIP_DTYPE_F32);
-        check(mhip_embedding_f32(ctx, table.f(), vocab, dim, ids.f(), num, out->f()));
+        check(table.compact
+                  ? mhip_embedding_bf16w_f32(ctx, table.h(), vocab, dim, ids.f(), num, out->f())
+                  : mhip_embedding_f32(ctx, table.f(), vocab, dim, ids.f(), num, out->f()));
         if (capture) {
             // A captured step checks its ids on the host at each replay and
             // the flag after its first run.
@@ -539,9 +544,16 @@ struct mhip_executor {
         require_f32(b, "matmul's b");
         if (addend) require_f32(*addend, "a fused matmul's addend");
         BufferPtr out = alloc_output(offered, Shape{m, n}, MHIP_DTYPE_F32);
-        check(mhip_matmul_f32(ctx, a.f(), b.f(), out->f(), m, k, n, ta, tb,
-                              addend ? addend->f() : nullptr, addend_mode));
+        check(matmul(a, b, out->f(), m, k, n, ta, tb, addend ? addend->f() : nullptr, addend_mode));
         return out;
+    }
+
+    // A product whose b is an f32 or a compact weight.
+    mhip_status matmul(const Buffer& a, const Buffer& b, float* out, uint64_t m, uint64_t k,
+                       uint64_t n, bool ta, bool tb, const float* addend, int mode) {
+        if (b.compact)
+            return mhip_matmul_bf16w_f32(ctx, a.f(), b.h(), out, m, k, n, ta, tb, addend, mode);
+        return mhip_matmul_f32(ctx, a.f(), b.f(), out, m, k, n, ta, tb, addend, mode);
     }
 
     static std::tuple<uint64_t, uint64_t, uint64_t> matmul_dims(const Buffer& a, const Buffer& b,
@@ -586,8 +598,8 @@ struct mhip_executor {
         require_f32(up, "gated-matmul");
         Buffer g(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
         Buffer u(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
-        check(mhip_matmul_f32(ctx, a.f(), gate.f(), g.f(), m, k, n, ta, tb, nullptr, 0));
-        check(mhip_matmul_f32(ctx, a.f(), up.f(), u.f(), m, k, n, ta, tb, nullptr, 0));
+        check(matmul(a, gate, g.f(), m, k, n, ta, tb, nullptr, 0));
+        check(matmul(a, up, u.f(), m, k, n, ta, tb, nullptr, 0));
         BufferPtr out = alloc_output(offered, Shape{m, n}, MHIP_DTYPE_F32);
         check(mhip_silu_mul_f32(ctx, g.f(), u.f(), out->f(), m * n));
         check(mhip_sync(ctx));  // the temporaries are freed on return
@@ -782,6 +794,7 @@ struct mhip_executor {
 
     BufferPtr clone(const Buffer& b) {
         BufferPtr copy = std::make_unique<Buffer>(ctx, b.bytes, b.shape, b.dtype);
+        copy->compact = b.compact;
         check(mhip_copy(ctx, copy->ptr, b.ptr, b.bytes));
         return copy;
     }
@@ -791,6 +804,7 @@ struct mhip_executor {
     // history), otherwise into a copy stored under the output. The store goes
     // back under the output id either way; a failed write leaves its rows.
     void run_kv_write(const Invocation& inv) {
+        expand_compact_inputs(inv);
         const std::optional<uint64_t> row_offset = attr_integer(inv, "row_offset");
         if (!row_offset) raise(MHIP_KERNEL_ATTRIBUTE_UNSUPPORTED, "row_offset");
         if (inv.inputs.size() < 1) raise(MHIP_KERNEL_EXECUTION_FAILED, "missing input at index 0");
@@ -833,10 +847,44 @@ struct mhip_executor {
         if (code != MHIP_KERNEL_OK) raise(code, error);
     }
 
+    // The same values as a compact buffer, stored as f32 (widened on the
+    // device).
+    BufferPtr expand(const Buffer& b) {
+        const uint64_t n = numel(b.shape);
+        BufferPtr f = std::make_unique<Buffer>(ctx, n * 4, b.shape, MHIP_DTYPE_F32);
+        check(mhip_decode_half(ctx, b.h(), f->f(), n, MHIP_BF16));
+        return f;
+    }
+
+    // expand_unsupported_compact_inputs (src/executor.rs:1323-1364): every
+    // compact input is stored as f32 for good unless the Kernel reads it
+    // compact -- the matmul family's b, gated-matmul's gate and up, the
+    // embedding lookup's table.
+    void expand_compact_inputs(const Invocation& inv) {
+        const std::string& name = inv.kernel;
+        auto reads_compact = [&](size_t index) {
+            if (name == "matmul" || name == "matmul-bias" || name == "matmul-residual") return index == 1;
+            if (name == "gated-matmul") return index == 1 || index == 2;
+            if (name == "embedding") return index == 0;
+            return false;
+        };
+        for (size_t i = 0; i < inv.inputs.size(); ++i) {
+            auto it = storage.find(inv.inputs[i].id);
+            if (reads_compact(i) || it == storage.end() || !it->second->compact) continue;
+            try {
+                it->second = expand(*it->second);
+            } catch (const KernelFailure& f) {
+                raise(MHIP_KERNEL_EXECUTION_FAILED,
+                      "expanding compact input " + std::to_string(i) + " of " + name + ": " + f.detail);
+            }
+        }
+    }
+
     // run_invocation_uncaptured (src/executor.rs:1268-1321): the overwritten
     // output's buffer is offered unless an input reads it; on failure it is
     // put back so the resource keeps its value.
     void run(const Invocation& inv) {
+        expand_compact_inputs(inv);
         if (inv.kernel == "kv-write") {
             run_kv_write(inv);
             record(inv);
@@ -1066,6 +1114,64 @@ mhip_kernel_error mhip_executor_write_zeroed_kv_store(mhip_executor* ex, const c
     });
 }
 
+namespace {
+
+// Downloads `count` values of a compact buffer from value `first` on and
+// widens them to f32 on the host.
+void download_widened(mhip_ctx* ctx, const Buffer& b, uint64_t first, uint64_t count, float* dst) {
+    std::vector<uint16_t> bits(count);
+    if (count) check(mhip_download(ctx, bits.data(), b.h() + first, count * 2));
+    for (uint64_t i = 0; i < count; ++i) {
+        const uint32_t u = static_cast<uint32_t>(bits[i]) << 16;
+        std::memcpy(dst + i, &u, 4);
+    }
+}
+
+}  // namespace
+
+mhip_kernel_error mhip_executor_write_weight_tensor(mhip_executor* ex, const char* id,
+                                                    const uint64_t* shape, int rank,
+                                                    const float* values, int* compact) {
+    return guarded([&] {
+        if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
+        if (compact) *compact = 0;
+        Shape s = make_shape(shape, rank);
+        const uint64_t n = numel(s);
+        if (n && !values) raise(MHIP_KERNEL_EXECUTION_FAILED, "null values");
+        // Compact when a matrix of at least 65536 values holds only exact bf16
+        // values (src/kernels.rs:1672-1690); lossless either way.
+        bool exact = s.size() == 2 && n >= (1u << 16);
+        for (uint64_t i = 0; exact && i < n; ++i) {
+            uint32_t u;
+            std::memcpy(&u, values + i, 4);
+            exact = (u & 0xFFFFu) == 0;
+        }
+        std::lock_guard<std::mutex> lock(ex->mu);
+        if (!exact) {
+            auto buf = std::make_unique<Buffer>(ex->ctx, n * 4, s, MHIP_DTYPE_F32);
+            if (n) check(mhip_upload(ex->ctx, buf->ptr, values, n * 4));
+            ex->storage[id] = std::move(buf);
+            return;
+        }
+        auto buf = std::make_unique<Buffer>(ex->ctx, n * 2, s, MHIP_DTYPE_F32);
+        buf->compact = true;
+        // Converted and uploaded a chunk at a time, bounding the host copy.
+        constexpr uint64_t kChunk = 1u << 20;
+        std::vector<uint16_t> bits(std::min<uint64_t>(n, kChunk));
+        for (uint64_t first = 0; first < n; first += kChunk) {
+            const uint64_t count = std::min<uint64_t>(kChunk, n - first);
+            for (uint64_t i = 0; i < count; ++i) {
+                uint32_t u;
+                std::memcpy(&u, values + first + i, 4);
+                bits[i] = static_cast<uint16_t>(u >> 16);
+            }
+            check(mhip_upload(ex->ctx, buf->h() + first, bits.data(), count * 2));
+        }
+        ex->storage[id] = std::move(buf);
+        if (compact) *compact = 1;
+    });
+}
+
 mhip_kernel_error mhip_executor_read_tensor(mhip_executor* ex, const char* id, void* dst,
                                             size_t capacity, size_t* written) {
     return guarded([&] {
@@ -1075,6 +1181,15 @@ mhip_kernel_error mhip_executor_read_tensor(mhip_executor* ex, const char* id, v
         if (it == ex->storage.end())
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + id);
         const Buffer& b = *it->second;
+        if (b.compact) {
+            const uint64_t n = numel(b.shape);
+            if (capacity < n * 4)
+                raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "destination holds " + std::to_string(capacity) +
+                                                         " bytes, tensor has " + std::to_string(n * 4));
+            download_widened(ex->ctx, b, 0, n, static_cast<float*>(dst));
+            if (written) *written = n * 4;
+            return;
+        }
         if (capacity < b.bytes)
             raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "destination holds " + std::to_string(capacity) +
                                                      " bytes, tensor has " + std::to_string(b.bytes));
@@ -1096,7 +1211,9 @@ mhip_kernel_error mhip_executor_read_tensor_values(mhip_executor* ex, const char
         if (capacity < n)
             raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "destination holds " + std::to_string(capacity) +
                                                      " values, tensor has " + std::to_string(n));
-        if (b.dtype == MHIP_DTYPE_F32) {
+        if (b.compact) {
+            download_widened(ex->ctx, b, 0, n, dst);
+        } else if (b.dtype == MHIP_DTYPE_F32) {
             check(mhip_download(ex->ctx, dst, b.ptr, n * 4));
         } else {
             Buffer tmp(ex->ctx, n * 4, b.shape, MHIP_DTYPE_F32);
@@ -1126,7 +1243,10 @@ mhip_kernel_error mhip_executor_read_tensor_rows(mhip_executor* ex, const char* 
                   "rows [" + std::to_string(row_begin) + ", " + std::to_string(row_begin + row_count) +
                       ") are outside the " + std::to_string(rows) + " rows");
         if (capacity < row_count * width) raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "destination too small");
-        check(mhip_download(ex->ctx, dst, b.f() + row_begin * width, row_count * width * 4));
+        if (b.compact)
+            download_widened(ex->ctx, b, row_begin * width, row_count * width, dst);
+        else
+            check(mhip_download(ex->ctx, dst, b.f() + row_begin * width, row_count * width * 4));
     });
 }
 
@@ -1167,6 +1287,7 @@ mhip_kernel_error mhip_executor_copy_tensor(mhip_executor* ex, const char* src, 
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + src);
         const Buffer& b = *it->second;
         auto copy = std::make_unique<Buffer>(ex->ctx, b.bytes, b.shape, b.dtype);
+        copy->compact = b.compact;
         check(mhip_copy(ex->ctx, copy->ptr, b.ptr, b.bytes));
         ex->storage[dst] = std::move(copy);
     });
@@ -1232,6 +1353,27 @@ mhip_status mhip_executor_observation(mhip_executor* ex, uint64_t index, mhip_ob
     std::snprintf(out->invocation, sizeof(out->invocation), "%s", o.invocation.c_str());
     out->error = o.error;
     return MHIP_OK;
+}
+
+mhip_kernel_error mhip_executor_select_greedy_column(mhip_executor* ex, const char* logits,
+                                                     uint64_t row, const uint64_t* excluded,
+                                                     uint32_t range_count, float temperature,
+                                                     int64_t* column) {
+    return guarded([&] {
+        if (!ex || !logits || !column) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor, id or result");
+        *column = -1;
+        std::lock_guard<std::mutex> lock(ex->mu);
+        auto it = ex->storage.find(logits);
+        if (it == ex->storage.end())
+            raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + logits);
+        const Buffer& b = *it->second;
+        mhip_executor::require_f32(b, "greedy selection's logits");
+        if (b.shape.empty()) raise(MHIP_KERNEL_SHAPE_UNSUPPORTED, "logits have no columns");
+        const uint64_t cols = b.shape.back();
+        const uint64_t rows = cols ? numel(b.shape) / cols : 0;
+        check(mhip_greedy_select_f32(ex->ctx, b.f(), rows, cols, row, excluded, range_count,
+                                     temperature, column));
+    });
 }
 
 // ---- step capture (src/executor.rs:177-336) ----

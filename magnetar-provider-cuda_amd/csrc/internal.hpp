@@ -19,13 +19,15 @@ namespace mhip {
 // and leaves that row of both outputs unwritten, as the embedding does.
 // Requires dim % 4 == 0, 16-byte aligned buffers and dim <= 16384; returns
 // MHIP_LAYOUT_UNSUPPORTED otherwise (the caller then runs the two calls).
-mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const float* table, uint64_t vocab, uint64_t dim,
+// `table` is f32, or bf16 bit patterns when `bf16_table`.
+mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const void* table, uint64_t vocab, uint64_t dim,
                               const float* ids, uint64_t rows, const float* weight, float eps,
-                              float* out, float* h);
+                              float* out, float* h, bool bf16_table = false);
 
-// One decode projection: out[rows, n] = a[rows, k] . b[k, n].
+// One decode projection: out[rows, n] = a[rows, k] . b[k, n]; b is f32, or
+// bf16 bit patterns when the set's weights are compact.
 struct GemvTarget {
-    const float* b;
+    const void* b;
     uint64_t n;
     float* out;
     // While capturing with MHIP_ADVANCE_ROW_OFFSET: the rows written move
@@ -50,7 +52,7 @@ enum GemvEpilogue : int {
 // interleaved form; the caller then runs the separate calls.
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                          const GemvTarget* targets, int count, int epilogue,
-                         const mhip_rope_params* rope);
+                         const mhip_rope_params* rope, bool bf16_weights = false);
 
 // While capturing: records that `what` cannot be captured and returns
 // MHIP_CAPTURE_UNSUPPORTED; MHIP_OK otherwise.

@@ -71,11 +71,15 @@ struct TileCfg {
     static_assert(kBRows * kBCols % (4 * kThreads) == 0, "B slice must split evenly");
 };
 
+using mhip::elem;
+using mhip::load4;
+using mhip::load4_nt;
+
 // Loads this thread's chunks of a (ROWS x COLS) slice whose columns are
 // contiguous in memory (leading dimension ld), rows from r0 and columns from
 // c0, zero-filling outside (rows_total, cols_total).
-template <int ROWS, int COLS, int CHUNKS, int THREADS, bool VEC>
-__device__ __forceinline__ void load_slice(float4 (&regs)[CHUNKS], const float* __restrict__ g,
+template <int ROWS, int COLS, int CHUNKS, int THREADS, bool VEC, class T>
+__device__ __forceinline__ void load_slice(float4 (&regs)[CHUNKS], const T* __restrict__ g,
                                            uint64_t ld, uint64_t r0, uint64_t c0,
                                            uint64_t rows_total, uint64_t cols_total) {
     constexpr int kChunksPerRow = COLS / 4;
@@ -87,14 +91,14 @@ __device__ __forceinline__ void load_slice(float4 (&regs)[CHUNKS], const float* 
         const uint64_t gr = r0 + r, gc = c0 + c;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (gr < rows_total) {
-            const float* p = g + gr * ld + gc;
+            const T* p = g + gr * ld + gc;
             if (VEC && gc + 3 < cols_total) {
-                v = *reinterpret_cast<const float4*>(p);
+                v = load4(p);
             } else {
-                if (gc + 0 < cols_total) v.x = p[0];
-                if (gc + 1 < cols_total) v.y = p[1];
-                if (gc + 2 < cols_total) v.z = p[2];
-                if (gc + 3 < cols_total) v.w = p[3];
+                if (gc + 0 < cols_total) v.x = elem(p + 0);
+                if (gc + 1 < cols_total) v.y = elem(p + 1);
+                if (gc + 2 < cols_total) v.z = elem(p + 2);
+                if (gc + 3 < cols_total) v.w = elem(p + 3);
             }
         }
         regs[i] = v;
@@ -144,9 +148,9 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
 // blockIdx.y is the k split: the workgroup sums k in [y * k_split,
 // min(K, (y + 1) * k_split)) and, with more than one split, writes that
 // partial product to C + y * M * N (no addend) for splitk_reduce_kernel.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
 __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, uint64_t M,
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
     uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     constexpr int T = Cfg::kThreads;
@@ -298,8 +302,8 @@ uint64_t choose_splits(uint64_t tiles, uint64_t k, uint64_t slots, uint64_t bk,
     return (k + per - 1) / per;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T>
-mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t m,
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT>
+mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
                         uint64_t k, uint64_t n, const float* addend, int mode, bool vec) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
@@ -316,20 +320,20 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const float* b, float* c,
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
     if (!configured) {
         (void)hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true>),
+            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         (void)hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false>),
+            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
     if (vec)
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, k_split);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, k_split);
     mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
@@ -355,9 +359,9 @@ constexpr int kGemvCols = 256;  // columns per workgroup: 64 lanes x 4
 // and k slice `slice`. Its 4 waves split the slice's rows and meet in LDS.
 // `direct`: write C (+ addend) itself (the only slice); otherwise write the
 // slice's partial sums for the reduction.
-template <int ROWS>
+template <int ROWS, class BT>
 __device__ __forceinline__ void gemv_partial_body(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ partial,
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t cg,
     uint32_t slice, bool direct, const float* __restrict__ addend, int addend_mode) {
     __shared__ float4 red[4][ROWS][64];
@@ -376,7 +380,7 @@ __device__ __forceinline__ void gemv_partial_body(
             float4 bv[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u)
-                bv[u] = mhip::load_nt(reinterpret_cast<const float4*>(B + (kk + 4 * u) * N + col));
+                bv[u] = load4_nt(B + (kk + 4 * u) * N + col);
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
 #pragma unroll
@@ -390,7 +394,7 @@ __device__ __forceinline__ void gemv_partial_body(
             }
         }
         for (; kk < k_end; kk += 4) {
-            const float4 bv = mhip::load_nt(reinterpret_cast<const float4*>(B + kk * N + col));
+            const float4 bv = load4_nt(B + kk * N + col);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const float a = A[r * K + kk];
@@ -428,12 +432,12 @@ __device__ __forceinline__ void gemv_partial_body(
     }
 }
 
-template <int ROWS>
+template <int ROWS, class BT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ partial,
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
     const float* __restrict__ addend, int addend_mode) {
-    gemv_partial_body<ROWS>(A, B, partial, C, K, N, k_per_slice, blockIdx.x, blockIdx.y,
+    gemv_partial_body<ROWS, BT>(A, B, partial, C, K, N, k_per_slice, blockIdx.x, blockIdx.y,
                             slices == 1, addend, addend_mode);
 }
 
@@ -515,7 +519,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
 // ---------------------------------------------------------------------------
 
 struct GemvSeg {
-    const float* b;
+    const void* b;  // f32, or bf16 bits (the set's element type)
     float* partial;
     float* out;
     const uint64_t* out_advance;  // captured step: rows of `out` move by the replay offset
@@ -548,7 +552,7 @@ __device__ __forceinline__ GemvSeg pick(const GemvSet& set, int i) {
     return set.seg[2];
 }
 
-template <int ROWS>
+template <int ROWS, class BT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const float* __restrict__ A,
                                                                         uint64_t K, GemvSet set) {
     const uint32_t b = blockIdx.x;
@@ -556,7 +560,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const fl
                   : (set.count > 1 && b >= set.seg[1].first_block) ? 1 : 0;
     const GemvSeg s = pick(set, i);
     const uint32_t local = b - s.first_block;
-    gemv_partial_body<ROWS>(A, s.b, s.partial, nullptr, K, s.n, s.k_per_slice,
+    gemv_partial_body<ROWS, BT>(A, static_cast<const BT*>(s.b), s.partial, nullptr, K, s.n, s.k_per_slice,
                             local % s.col_groups, local / s.col_groups, false, nullptr, 0);
 }
 
@@ -637,8 +641,8 @@ void gemv_slicing(const mhip_ctx* ctx, uint64_t k, uint64_t n, uint64_t* slices_
     *k_per_slice_out = k_per_slice;
 }
 
-template <int ROWS>
-mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t k,
+template <int ROWS, class BT>
+mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t k,
                         uint64_t n, const float* addend, int mode) {
     const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
     uint64_t slices, k_per_slice;
@@ -648,7 +652,7 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c,
         mhip_status st = workspace(ctx, slices * ROWS * n * sizeof(float), &partial);
         if (st != MHIP_OK) return st;
     }
-    hipLaunchKernelGGL(gemv_partial_kernel<ROWS>,
+    hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT>),
                        dim3(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices)),
                        dim3(kGemvThreads), 0, ctx->stream, a, b, partial, c, k, n, k_per_slice,
                        static_cast<uint32_t>(slices), addend, mode);
@@ -660,12 +664,12 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c,
     return mhip::check_launch("matmul (decode reduction)");
 }
 
-template <int ROWS>
+template <int ROWS, class BT>
 mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
                             const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups) {
     uint32_t blocks = 0;
     for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
-    hipLaunchKernelGGL(gemv_set_partial_kernel<ROWS>, dim3(blocks), dim3(kGemvThreads), 0,
+    hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT>), dim3(blocks), dim3(kGemvThreads), 0,
                        ctx->stream, a, k, set);
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
@@ -674,17 +678,18 @@ mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet s
     return mhip::check_launch("decode projections (reduction)");
 }
 
-mhip_status dispatch_gemv(mhip_ctx* ctx, const float* a, const float* b, float* c, uint64_t m,
+template <class BT>
+mhip_status dispatch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
                           uint64_t k, uint64_t n, const float* addend, int mode) {
     switch (m) {
-        case 1: return launch_gemv<1>(ctx, a, b, c, k, n, addend, mode);
-        case 2: return launch_gemv<2>(ctx, a, b, c, k, n, addend, mode);
-        case 3: return launch_gemv<3>(ctx, a, b, c, k, n, addend, mode);
-        case 4: return launch_gemv<4>(ctx, a, b, c, k, n, addend, mode);
-        case 5: return launch_gemv<5>(ctx, a, b, c, k, n, addend, mode);
-        case 6: return launch_gemv<6>(ctx, a, b, c, k, n, addend, mode);
-        case 7: return launch_gemv<7>(ctx, a, b, c, k, n, addend, mode);
-        default: return launch_gemv<8>(ctx, a, b, c, k, n, addend, mode);
+        case 1: return launch_gemv<1, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 2: return launch_gemv<2, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 3: return launch_gemv<3, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 4: return launch_gemv<4, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 5: return launch_gemv<5, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 6: return launch_gemv<6, BT>(ctx, a, b, c, k, n, addend, mode);
+        case 7: return launch_gemv<7, BT>(ctx, a, b, c, k, n, addend, mode);
+        default: return launch_gemv<8, BT>(ctx, a, b, c, k, n, addend, mode);
     }
 }
 
@@ -699,11 +704,12 @@ __global__ void fill_addend_kernel(float* C, uint64_t M, uint64_t N, const float
     C[idx] = v;
 }
 
-}  // namespace
-
-extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
-                                       uint64_t m, uint64_t k, uint64_t n, int transpose_a,
-                                       int transpose_b, const float* addend, int addend_mode) {
+// The shared body of the f32 and compact-weight matmuls: B as f32 or as bf16
+// bit patterns; everything else (A, C, the addend, the arithmetic) is f32.
+template <class BT>
+mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, uint64_t m,
+                        uint64_t k, uint64_t n, int transpose_a, int transpose_b,
+                        const float* addend, int addend_mode) {
     MHIP_REQUIRE_CTX(ctx);
     if (addend_mode < 0 || addend_mode > 2)
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul addend mode must be 0, 1 or 2");
@@ -717,25 +723,64 @@ extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const floa
         return mhip::check_launch("matmul (empty inner dimension)");
     }
     const bool ta = transpose_a != 0, tb = transpose_b != 0;
-    if (m <= kGemvMaxRows && !ta && !tb && n % 4 == 0 && mhip::aligned16(b))
-        return dispatch_gemv(ctx, a, b, out, m, k, n, addend, addend_mode);
-    // Vector loads need 16-byte aligned rows on both operands.
+    // B's vector accesses (dwordx4 of f32, or 8 bytes of bf16) need rows of a
+    // multiple of 4 elements and an aligned base.
+    const uintptr_t b_align = sizeof(BT) == 4 ? 15u : 7u;
+    const bool b_aligned = (reinterpret_cast<uintptr_t>(b) & b_align) == 0;
+    if (m <= kGemvMaxRows && !ta && !tb && n % 4 == 0 && b_aligned)
+        return dispatch_gemv<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
-    const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && mhip::aligned16(b);
+    const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
     if (!ta && !tb)
-        return launch_mfma<128, 128, 32, 64, 64, false, false>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (ta && !tb)
-        return launch_mfma<128, 128, 32, 64, 64, true, false>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        return launch_mfma<128, 128, 32, 64, 64, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (!ta && tb)
-        return launch_mfma<128, 128, 32, 64, 64, false, true>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-    return launch_mfma<128, 128, 32, 64, 64, true, true>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        return launch_mfma<128, 128, 32, 64, 64, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+    return launch_mfma<128, 128, 32, 64, 64, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
 }
+
+}  // namespace
+
+extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
+                                       uint64_t m, uint64_t k, uint64_t n, int transpose_a,
+                                       int transpose_b, const float* addend, int addend_mode) {
+    return matmul_impl<float>(ctx, a, b, out, m, k, n, transpose_a, transpose_b, addend, addend_mode);
+}
+
+extern "C" mhip_status mhip_matmul_bf16w_f32(mhip_ctx* ctx, const float* a, const uint16_t* b,
+                                             float* out, uint64_t m, uint64_t k, uint64_t n,
+                                             int transpose_a, int transpose_b, const float* addend,
+                                             int addend_mode) {
+    return matmul_impl<uint16_t>(ctx, a, b, out, m, k, n, transpose_a, transpose_b, addend,
+                                 addend_mode);
+}
+
+namespace {
+
+template <class BT>
+mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
+                              const GemvSet& set, int epilogue, const RopeEpi& rq,
+                              const RopeEpi& rk, uint32_t g) {
+    switch (rows) {
+        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        default: return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+    }
+}
+
+}  // namespace
 
 namespace mhip {
 
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                          const GemvTarget* targets, int count, int epilogue,
-                         const mhip_rope_params* rope) {
+                         const mhip_rope_params* rope, bool bf16_weights) {
     MHIP_REQUIRE_CTX(ctx);
     if (!a || !targets || count < 1 || count > 3 || rows == 0 || rows > kGemvMaxRows || k == 0)
         return MHIP_LAYOUT_UNSUPPORTED;
@@ -749,7 +794,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     for (int i = 0; i < count; ++i) {
         const GemvTarget& t = targets[i];
         const bool needs_out = !(epilogue == kGemvSiluMul && i == 1);
-        if (!t.b || t.n == 0 || t.n % 4 != 0 || !aligned16(t.b) ||
+        const uintptr_t b_align = bf16_weights ? 7u : 15u;
+        if (!t.b || t.n == 0 || t.n % 4 != 0 || (reinterpret_cast<uintptr_t>(t.b) & b_align) != 0 ||
             (needs_out && (!t.out || !aligned16(t.out))))
             return MHIP_LAYOUT_UNSUPPORTED;
         GemvSeg& g = set.seg[i];
@@ -803,16 +849,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     float* partial = static_cast<float*>(scratch);
     for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
     const uint32_t g = static_cast<uint32_t>(groups);
-    switch (rows) {
-        case 1: return launch_gemv_set<1>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 2: return launch_gemv_set<2>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 3: return launch_gemv_set<3>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 4: return launch_gemv_set<4>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 5: return launch_gemv_set<5>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 6: return launch_gemv_set<6>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 7: return launch_gemv_set<7>(ctx, a, k, set, epilogue, rq, rk, g);
-        default: return launch_gemv_set<8>(ctx, a, k, set, epilogue, rq, rk, g);
-    }
+    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g)
+                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g);
 }
 
 }  // namespace mhip

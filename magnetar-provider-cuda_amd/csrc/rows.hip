@@ -55,9 +55,9 @@ __device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
 // With `ids` set, row r of the input is row ids[r] of `in` (an embedding
 // table of `vocab` rows) and is also copied to `copy` row r: the embedding
 // lookup and the RMSNorm of its output in one pass.
-template <int G, int VPT>
+template <int G, int VPT, class TT = float>
 __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
-    const float* __restrict__ in, const float* __restrict__ weight, float* __restrict__ out,
+    const TT* __restrict__ in, const float* __restrict__ weight, float* __restrict__ out,
     uint64_t rows, uint64_t cols, uint64_t weight_row_stride, float eps,
     const float* __restrict__ ids, uint64_t vocab, float* __restrict__ copy, uint32_t* flags) {
 #pragma clang fp contract(off)
@@ -72,13 +72,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
         if (lane == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
         live = false;  // still takes part in the group reduction below
     }
-    const float4* x4 = reinterpret_cast<const float4*>(in) + src * cols4;
+    const TT* xr = in + src * cols;
     float4 x[VPT];
     float ss = 0.0f;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        x[v] = (live && c < cols4) ? mhip::load_nt(x4 + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[v] = (live && c < cols4) ? mhip::load4_nt(xr + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
         ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
     }
     ss = group_reduce<G>(ss, SumOp{}, scratch);
@@ -194,21 +194,29 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(const float* in,
 
 enum class RowKind { Rms, Softmax };
 
-// Embedding gather for the RMSNorm kernel (unused by the other kinds).
+// Embedding gather for the RMSNorm kernel (unused by the other kinds); the
+// table is f32, or bf16 bit patterns when `bf16`.
 struct Gather {
     const float* ids = nullptr;
     uint64_t vocab = 0;
     float* copy = nullptr;
+    bool bf16 = false;
 };
 
 template <RowKind KIND, int G, int VPT>
 void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
                 uint64_t cols, uint64_t wstride, float eps, const Gather& g) {
     const unsigned blocks = static_cast<unsigned>(mhip::ceil_div(rows, kThreads / G));
-    if constexpr (KIND == RowKind::Rms)
-        hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
-                           ctx->stream, in, weight, out, rows, cols, wstride, eps, g.ids, g.vocab,
-                           g.copy, ctx->flags);
+    if constexpr (KIND == RowKind::Rms) {
+        if (g.bf16)
+            hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT, uint16_t>), dim3(blocks), dim3(kThreads),
+                               0, ctx->stream, reinterpret_cast<const uint16_t*>(in), weight, out,
+                               rows, cols, wstride, eps, g.ids, g.vocab, g.copy, ctx->flags);
+        else
+            hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT, float>), dim3(blocks), dim3(kThreads), 0,
+                               ctx->stream, in, weight, out, rows, cols, wstride, eps, g.ids,
+                               g.vocab, g.copy, ctx->flags);
+    }
     else
         hipLaunchKernelGGL((softmax_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
                            ctx->stream, in, out, rows, cols, ctx->flags);
@@ -277,20 +285,22 @@ mhip_status mhip_softmax_rows_f32(mhip_ctx* ctx, const float* in, float* out, ui
 
 namespace mhip {
 
-mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const float* table, uint64_t vocab, uint64_t dim,
+mhip_status embed_rmsnorm_f32(mhip_ctx* ctx, const void* table, uint64_t vocab, uint64_t dim,
                               const float* ids, uint64_t rows, const float* weight, float eps,
-                              float* out, float* h) {
+                              float* out, float* h, bool bf16_table) {
     MHIP_REQUIRE_CTX(ctx);
     if (rows == 0) return MHIP_OK;
+    const uintptr_t table_align = bf16_table ? 7u : 15u;
     if (dim == 0 || dim % 4 != 0 || dim / 4 > 4096 || !(eps > 0.0f) || !table || !ids || !out ||
-        !h || !aligned16(table) || !aligned16(out) || !aligned16(h) ||
+        !h || (reinterpret_cast<uintptr_t>(table) & table_align) != 0 || !aligned16(out) || !aligned16(h) ||
         (weight && !aligned16(weight)) || rows >= (1ULL << 31))
         return MHIP_LAYOUT_UNSUPPORTED;
     Gather g;
     g.ids = ids;
     g.vocab = vocab;
     g.copy = out;
-    dispatch_vec<RowKind::Rms>(ctx, rows, table, weight, h, dim, 0, eps, g);
+    g.bf16 = bf16_table;
+    dispatch_vec<RowKind::Rms>(ctx, rows, static_cast<const float*>(table), weight, h, dim, 0, eps, g);
     return check_launch("embedding + rmsnorm");
 }
 

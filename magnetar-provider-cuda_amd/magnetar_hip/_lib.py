@@ -139,6 +139,11 @@ SIGNATURES = {
     "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
     "mhip_attention_f32": [_CTX, _P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
     "mhip_kv_write_f32": [_CTX, _P, _U64, _U64, _P, _U64, _U64],
+    "mhip_matmul_bf16w_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, ctypes.c_int, ctypes.c_int, _P,
+                              ctypes.c_int],
+    "mhip_embedding_bf16w_f32": [_CTX, _P, _U64, _U64, _P, _U64, _P],
+    "mhip_greedy_select_f32": [_CTX, _P, _U64, _U64, _U64, _P, ctypes.c_uint32, ctypes.c_float,
+                               ctypes.POINTER(ctypes.c_int64)],
     "mhip_capture_begin": [_CTX, ctypes.c_uint32],
     "mhip_capture_end": [_CTX, ctypes.POINTER(_P), ctypes.POINTER(_U64)],
     "mhip_capture_abort": [_CTX],

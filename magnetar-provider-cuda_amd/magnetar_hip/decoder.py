@@ -15,7 +15,8 @@ class BlockConfig(ctypes.Structure):
     _fields_ = [("hidden", ctypes.c_uint64), ("heads", ctypes.c_uint64),
                 ("kv_heads", ctypes.c_uint64), ("head_dim", ctypes.c_uint64),
                 ("ffn", ctypes.c_uint64), ("vocab", ctypes.c_uint64),
-                ("eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
+                ("eps", ctypes.c_float), ("rope_base", ctypes.c_float),
+                ("weight_format", ctypes.c_uint32)]
 
 
 class BlockWeights(ctypes.Structure):
@@ -65,17 +66,36 @@ class Shapes:
                 "w_gate": (h, f), "w_up": (h, f), "w_down": (f, h)}
 
 
+def bf16_bits(values: np.ndarray) -> np.ndarray:
+    """The bf16 bit patterns of f32 values that are exactly bf16 values."""
+    u = np.ascontiguousarray(values, np.float32).view(np.uint32)
+    if np.any(u & 0xFFFF):
+        raise ValueError("values are not exact bf16 values")
+    return (u >> 16).astype(np.uint16)
+
+
 class DecoderBlock:
     def __init__(self, dev: Device, shapes: Shapes, weights: dict, cache_rows: int,
-                 max_seq: int):
+                 max_seq: int, bf16_weights: bool = False):
+        """`bf16_weights`: store the matrices compact, as bf16 bit patterns (host
+        values must be exact bf16 values; device arrays must hold the bits)."""
         self.dev, self.s, self.cache_rows = dev, shapes, cache_rows
-        self.w = {k: (v if isinstance(v, DeviceArray) else dev.upload(np.asarray(v, np.float32)))
-                  for k, v in weights.items()}
+
+        def place(name, v):
+            if isinstance(v, DeviceArray):
+                return v
+            v = np.asarray(v, np.float32)
+            if bf16_weights and not name.endswith("norm"):
+                return dev.upload(bf16_bits(v))
+            return dev.upload(v)
+
+        self.w = {k: place(k, v) for k, v in weights.items()}
         kv = shapes.kv_heads * shapes.head_dim
         self.k_cache = dev.zeros((cache_rows, kv))
         self.v_cache = dev.zeros((cache_rows, kv))
         self.cfg = BlockConfig(shapes.hidden, shapes.heads, shapes.kv_heads, shapes.head_dim,
-                               shapes.ffn, shapes.vocab, shapes.eps, shapes.rope_base)
+                               shapes.ffn, shapes.vocab, shapes.eps, shapes.rope_base,
+                               1 if bf16_weights else 0)
         self.cw = BlockWeights(*[self.w[n].ptr for n in WEIGHT_NAMES])
         self.ws_bytes = int(_bind().mhip_block_workspace_bytes(ctypes.byref(self.cfg), max_seq))
         self.ws = dev.empty((max(1, self.ws_bytes // 4),))

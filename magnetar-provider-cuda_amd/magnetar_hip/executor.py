@@ -99,6 +99,8 @@ _SIGS = {
     "mhip_executor_write_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t], ctypes.c_int),
     "mhip_executor_write_tensor_values": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
     "mhip_executor_write_zeroed_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, ctypes.c_int], ctypes.c_int),
+    "mhip_executor_write_weight_tensor": ([_P, ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.c_int, _P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "mhip_executor_select_greedy_column": ([_P, ctypes.c_char_p, _U64, _P, ctypes.c_uint32, ctypes.c_float, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
     "mhip_executor_supports_step_capture": ([_P], ctypes.c_int),
     "mhip_executor_begin_step_capture": ([_P, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int], ctypes.c_int),
     "mhip_executor_end_step_capture": ([_P, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_int),
@@ -284,6 +286,16 @@ class Executor:
         shp, rank = _shape(shape)
         _check(_lib_bound().mhip_executor_write_zeroed_tensor(self._h, id.encode(), shp, rank, dtype))
 
+    def write_weight_tensor(self, id: str, values: np.ndarray) -> bool:
+        """A weight (src/executor.rs:384-399): stored compact as bf16 bits when it
+        is a matrix of >= 65536 exact bf16 values; returns whether it was."""
+        v = np.ascontiguousarray(values, np.float32)
+        shp, rank = _shape(v.shape)
+        compact = ctypes.c_int(0)
+        _check(_lib_bound().mhip_executor_write_weight_tensor(
+            self._h, id.encode(), shp, rank, v.ctypes.data_as(_P), ctypes.byref(compact)))
+        return bool(compact.value)
+
     def write_zeroed_kv_store(self, id: str, shape: Sequence[int], precision: int = KV_F32,
                               head_dimension: int = 0) -> bool:
         """A zeroed KV store (src/executor.rs:560-602). True when stored; the
@@ -348,6 +360,18 @@ class Executor:
 
     def execute(self, inv: KernelInvocation) -> None:
         self.complete_kernel(self.submit_kernel(inv))
+
+    def select_greedy_column(self, logits: str, row: int = 0, excluded=(),
+                             temperature: float = 0.0):
+        """The greedy column of `logits` row `row` (src/executor.rs:2549-2564), or
+        None when no column is eligible or the selection fails, as the
+        reference's Option."""
+        flat = [int(v) for r in excluded for v in (r[0], r[1])]
+        ranges = (ctypes.c_uint64 * max(1, len(flat)))(*flat)
+        col = ctypes.c_int64(-1)
+        code = _lib_bound().mhip_executor_select_greedy_column(
+            self._h, logits.encode(), row, ranges, len(flat) // 2, temperature, ctypes.byref(col))
+        return None if code != 0 or col.value < 0 else int(col.value)
 
     # ---- step capture (src/executor.rs:177-336) ----
     def supports_step_capture(self) -> bool:

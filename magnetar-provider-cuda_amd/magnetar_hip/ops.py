@@ -173,3 +173,37 @@ def kv_write(dev: Device, store: DeviceArray, rows: DeviceArray, row_offset: int
         raise ValueError("kv-write rows must be [count, store width]")
     call("mhip_kv_write_f32", dev.ctx, _p(store), capacity, width, _p(rows), count, row_offset)
     return store
+
+
+def greedy_select(dev: Device, logits: DeviceArray, row: int = 0, excluded=(),
+                  temperature: float = 0.0):
+    """Greedy column of `logits` row `row`, or None (mhip_greedy_select_f32)."""
+    cols = logits.shape[-1]
+    rows = logits.size // max(1, cols)
+    flat = [int(v) for r in excluded for v in (r[0], r[1])]
+    ranges = (ctypes.c_uint64 * max(1, len(flat)))(*flat)
+    col = ctypes.c_int64(-1)
+    call("mhip_greedy_select_f32", dev.ctx, _p(logits), rows, cols, row, ranges, len(flat) // 2,
+         temperature, ctypes.byref(col))
+    return None if col.value < 0 else int(col.value)
+
+
+def matmul_bf16w(dev: Device, a: DeviceArray, b_bits: DeviceArray, transpose_a: bool = False,
+                 transpose_b: bool = False, addend: DeviceArray | None = None,
+                 addend_mode: int = 0, out=None) -> DeviceArray:
+    """matmul with a compact weight: b as bf16 bit patterns (uint16)."""
+    m, k = (a.shape[1], a.shape[0]) if transpose_a else (a.shape[0], a.shape[1])
+    k2, n = (b_bits.shape[1], b_bits.shape[0]) if transpose_b else (b_bits.shape[0], b_bits.shape[1])
+    if k != k2:
+        raise ValueError(f"matmul inner dimension mismatch: {k} vs {k2}")
+    out = _out(dev, out, (m, n))
+    call("mhip_matmul_bf16w_f32", dev.ctx, _p(a), _p(b_bits), _p(out), m, k, n, int(transpose_a),
+         int(transpose_b), _p(addend), addend_mode)
+    return out
+
+
+def embedding_bf16w(dev: Device, table_bits: DeviceArray, ids: DeviceArray, out=None) -> DeviceArray:
+    vocab, dim = table_bits.shape
+    out = _out(dev, out, (ids.size, dim))
+    call("mhip_embedding_bf16w_f32", dev.ctx, _p(table_bits), vocab, dim, _p(ids), ids.size, _p(out))
+    return out

@@ -529,3 +529,24 @@ int orc_attention(const float* q, const float* k, const float* v, float* out,
                   const orc_attention_params* p) {
     return orc_attention_heads(q, k, v, out, p, 0, p->head_count);
 }
+
+/* src/kernels.cu:1808-1866 (greedy_select_kernel's contract). */
+int64_t orc_greedy_select(const float* row, uint64_t cols, const uint64_t* ranges,
+                          uint32_t range_count, float temperature) {
+    int64_t best = -1;
+    float best_value = 0.0f;
+    for (uint64_t i = 0; i < cols; ++i) {
+        float value = row[i];
+        if (!isfinite(value)) continue;
+        int excluded = 0;
+        for (uint32_t r = 0; r < range_count; ++r)
+            if (i >= ranges[2 * r] && i < ranges[2 * r + 1]) excluded = 1;
+        if (excluded) continue;
+        if (temperature != 0.0f) value = value / temperature;
+        if (best < 0 || value > best_value) {
+            best = (int64_t)i;
+            best_value = value;
+        }
+    }
+    return best;
+}

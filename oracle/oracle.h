@@ -122,6 +122,14 @@ int orc_attention_heads(const float* q, const float* k, const float* v, float* o
                         const orc_attention_params* p, uint64_t head_begin,
                         uint64_t head_end);
 
+/* Greedy next-token selection (src/kernels.cu:1808-1866): the column of the
+ * largest score / temperature (score when temperature is 0) among finite
+ * scores outside the [start, end) pairs of `ranges`; ties to the lowest
+ * column. -1 when none is eligible. Restated as an ascending scan with a
+ * strict comparison, not the reference's key encoding. */
+int64_t orc_greedy_select(const float* row, uint64_t cols, const uint64_t* ranges,
+                          uint32_t range_count, float temperature);
+
 #ifdef __cplusplus
 }
 #endif

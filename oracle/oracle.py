@@ -89,12 +89,14 @@ _SIGS = {
     "orc_matmul_rows": [_P, _P, _P, _U64, _U64, _U64, _U64],
     "orc_attention": [_P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
     "orc_attention_heads": [_P, _P, _P, _P, ctypes.POINTER(AttentionParams), _U64, _U64],
+    "orc_greedy_select": [_P, _U64, _P, ctypes.c_uint32, _F],
 }
 _RES = {
     "orc_f16_to_f32": ctypes.c_float,
     "orc_bf16_to_f32": ctypes.c_float,
     "orc_f32_to_f16": ctypes.c_uint16,
     "orc_f32_to_bf16": ctypes.c_uint16,
+    "orc_greedy_select": ctypes.c_int64,
 }
 _VOID = {"orc_hashed_values", "orc_values", "orc_attention_values", "orc_uniform", "orc_normal",
          "orc_token_ids", "orc_encode_f16", "orc_encode_bf16", "orc_decode_f16",
@@ -338,3 +340,12 @@ def attention(q, k, v, params: AttentionParams, heads=None):
         st = lib().orc_attention_heads(_ptr(q), _ptr(k), _ptr(v), _ptr(out),
                                        ctypes.byref(params), heads[0], heads[1])
     return out, st
+
+
+def greedy_select(row, excluded=(), temperature=0.0):
+    """Column index or None (orc_greedy_select)."""
+    row = _f32(row).ravel()
+    flat = np.array([v for r in excluded for v in (r[0], r[1])] or [0, 0], np.uint64)
+    col = lib().orc_greedy_select(_ptr(row), row.size, _ptr(flat), len(excluded),
+                                  ctypes.c_float(temperature))
+    return None if col < 0 else int(col)

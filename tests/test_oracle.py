@@ -449,3 +449,34 @@ def test_attention_known_answers(orc, fx):
     assert orc.attention(q, k, v, orc.attention_params(5, 5, 3, 4, kv_head_count=2))[1] == 1
     assert orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, window_size=2))[1] == 1
     assert orc.attention(q, k, v, orc.attention_params(5, 5, 2, 4, key_count=4))[1] == 1
+
+
+# ---- greedy selection (src/kernels.cu:1808-1866) ----
+
+def test_greedy_select_known_answers(orc):
+    """Known answers that pin each rule: the maximum wins; ties go to the lowest
+    column; -0 ties +0; non-finite scores and excluded ranges are skipped;
+    temperature divides (a negative one flips the order); nothing eligible
+    gives None."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    assert orc.greedy_select([1.0, 3.0, 2.0]) == 1
+    assert orc.greedy_select([5.0, 1.0, 5.0]) == 0
+    assert orc.greedy_select([-0.0, 0.0, -1.0]) == 0
+    assert orc.greedy_select([0.0, -0.0]) == 0
+    assert orc.greedy_select([nan, inf, -inf, 1.0]) == 3
+    assert orc.greedy_select([9.0, 1.0, 8.0, 2.0], excluded=[(0, 1), (2, 3)]) == 3
+    assert orc.greedy_select([9.0, 1.0], excluded=[(0, 2)]) is None
+    assert orc.greedy_select([nan, inf]) is None
+    assert orc.greedy_select([1.0, 3.0, 2.0], temperature=-1.0) == 0
+    assert orc.greedy_select([1.0, 3.0, 2.0], temperature=0.5) == 1
+    assert orc.greedy_select([]) is None
+
+
+def test_greedy_select_matches_argmax_on_random_rows(orc):
+    """Without exclusions or non-finite values, greedy is numpy's argmax (which
+    also returns the first maximum)."""
+    rng = np.random.default_rng(3)
+    for n in (1, 7, 1000, 32000):
+        row = rng.standard_normal(n).astype(np.float32)
+        row[rng.integers(0, n, max(1, n // 50))] = row.max()  # planted ties
+        assert orc.greedy_select(row) == int(np.argmax(row))
