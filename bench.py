@@ -161,6 +161,12 @@ def matmul_cases(dev, orc):
     c = dev.empty((1, 11008))
     cases.append(Case("matmul_1x4096x11008", lambda i: ops.matmul(dev, a, bs[i % rb], out=c),
                       4 * (4096 * 11008 + 4096 + 11008), "hbm", [1, 4096, 11008]))
+    # The same product over a compact weight (bf16 bits, widened exactly).
+    rh = _copies(4096 * 11008 * 2)
+    hs = [_device_normal(dev, (4096, 11008), seed(2, 40 + i), 0.5, bf16=True) for i in range(rh)]
+    cases.append(Case("matmul_1x4096x11008_bf16w",
+                      lambda i: ops.matmul_bf16w(dev, a, hs[i % rh], out=c),
+                      2 * 4096 * 11008 + 4 * (4096 + 11008), "hbm", [1, 4096, 11008]))
     return cases
 
 
@@ -190,17 +196,21 @@ def attention_cases(dev, orc):
     return cases
 
 
-def _device_normal(dev, shape, s, std):
-    """A seeded N(0, std) device tensor, generated on the host in chunks."""
+def _device_normal(dev, shape, s, std, bf16=False):
+    """A seeded N(0, std) device tensor, generated on the host in chunks; with
+    `bf16`, stored as bf16 bit patterns (the f32 values truncated)."""
     import ctypes
     from oracle import oracle as orc
     from magnetar_hip._lib import call
-    arr = dev.empty(shape)
+    arr = dev.empty(shape, np.uint16 if bf16 else np.float32)
     n = int(np.prod(shape))
+    size = 2 if bf16 else 4
     chunk = 16 << 20
     for i0 in range(0, n, chunk):
         host = orc.normal(min(chunk, n - i0), s + i0, 0.0, std)
-        call("mhip_upload", dev.ctx, ctypes.c_void_p(arr.ptr + 4 * i0),
+        if bf16:
+            host = (host.view(np.uint32) >> 16).astype(np.uint16)
+        call("mhip_upload", dev.ctx, ctypes.c_void_p(arr.ptr + size * i0),
              host.ctypes.data_as(ctypes.c_void_p), host.nbytes)
     return arr
 
@@ -211,14 +221,15 @@ def decoder_cases(dev, orc):
     from magnetar_hip.decoder import DecoderBlock, Shapes
     cases = []
 
-    def block(shapes, cfg, cache_rows, max_seq):
+    def block(shapes, cfg, cache_rows, max_seq, bf16=False):
         w = {}
         for i, (name, shape) in enumerate(shapes.weight_shapes().items()):
             if name.endswith("norm"):
                 w[name] = dev.upload(np.ones(shape, np.float32))
             else:
-                w[name] = _device_normal(dev, shape, seed(cfg, 16 + i), 0.02)
-        return DecoderBlock(dev, shapes, w, cache_rows=cache_rows, max_seq=max_seq)
+                w[name] = _device_normal(dev, shape, seed(cfg, 16 + i), 0.02, bf16=bf16)
+        return DecoderBlock(dev, shapes, w, cache_rows=cache_rows, max_seq=max_seq,
+                            bf16_weights=bf16)
 
     tiny = Shapes(vocab=1024, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=688)
     b0 = block(tiny, 0, 32, 32)
@@ -256,6 +267,11 @@ def decoder_cases(dev, orc):
     g4 = dev.capture_end()
     cases.append(Case("decoder_c5_decode_kv2048_graph", lambda i: g4.launch(0),
                       weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
+    # Config 4 decode with compact bf16 weights (a bf16 checkpoint): half the
+    # weight bytes, the same f32 arithmetic.
+    b4h = block(big, 4, 2049, 1, bf16=True)
+    cases.append(Case("decoder_c5_decode_kv2048_bf16w", lambda i: b4h.forward(ids_d, 2048, out_d),
+                      weight_bytes // 2 + kv_bytes, "hbm", [1, 4096], tokens=1))
     return cases
 
 

@@ -374,7 +374,9 @@ __device__ __forceinline__ void gemv_partial_body(
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
-        constexpr int kU = 8;
+        // Rows of B in flight per lane: 8 dwordx4 of f32, 16 8-byte bf16 loads
+        // (the same bytes in flight either way).
+        constexpr int kU = sizeof(BT) == 4 ? 8 : 16;
         uint64_t kk = k_begin + wave;
         for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
             float4 bv[kU];
