@@ -91,21 +91,72 @@ template <int D, int VD>
 struct PrefillCfg {
     static constexpr int kBQ = 128;            // queries per workgroup (4 waves x 32)
     static constexpr int kBKV = 32;            // keys per tile
-    static constexpr int kSK = D + 4;          // LDS row stride of K (dwordx4 aligned)
-    static constexpr int kSV = VD + 4;
-    static constexpr int kTile = kBKV * kSK + kBKV * kSV;
-    static constexpr int kLdsFloats = 2 * kTile;
-    static constexpr int kKChunks = kBKV * D / 4 / 256;   // dwordx4 per thread
-    static constexpr int kVChunks = kBKV * VD / 4 / 256;
-    static_assert(kBKV * D % 1024 == 0 && kBKV * VD % 1024 == 0, "tile must split over 256 threads");
+    static constexpr int kKTile = kBKV * D;    // floats; rows unpadded, 16-byte chunks swizzled
+    static constexpr int kVTile = kBKV * VD;
+    static constexpr int kLdsFloats = 2 * kKTile + 2 * kVTile;  // K and V, double-buffered apart
 };
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// Rows [k0, k0 + 32) of a row-major [*, W] operand (leading dimension ld)
+// into an LDS tile of 32 x W floats, by direct global -> LDS loads: one
+// instruction fills 1 KB of consecutive 16-byte slots, lane i slot i. Slot
+// (row, c) holds the row's chunk c ^ (row & 7) (XOR swizzle instead of
+// padding, so reads down a column and across a row hit distinct banks). Rows
+// at or past `rows` repeat row rows - 1 (finite data the caller masks out).
+// Completion is tracked by vmcnt: wait for it before the tile's barrier.
+template <int W>
+__device__ __forceinline__ void dma_tile(const float* g, uint64_t ld, uint64_t k0, uint64_t rows,
+                                         float* tile, int wave, int lane) {
+    constexpr int kChunksPerRow = W / 4;
+    constexpr int kInstrPerWave = 32 * W / 4 / 64 / 4;
+    static_assert(kInstrPerWave >= 1 && kChunksPerRow >= 8, "tile must split over four waves");
+#pragma unroll
+    for (int j = 0; j < kInstrPerWave; ++j) {
+        const int slot0 = (wave * kInstrPerWave + j) * 64;
+        const int slot = slot0 + lane;
+        const int row = slot / kChunksPerRow;
+        const int chunk = (slot % kChunksPerRow) ^ (row & 7);
+        uint64_t key = k0 + row;
+        if (key >= rows) key = rows - 1;
+        const float* src = g + key * ld + chunk * 4;
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
+    }
+}
+
+// S^T[key][query] of one tile: A = the K rows (lane -> key l32), B = Q^T.
+template <int D>
+__device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D / 2], int l32,
+                                            int half) {
+    v16f s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    const float* krow = sk + l32 * D;
+    const int swz = l32 & 7;
+#pragma unroll
+    for (int t = 0; t < D / 2; t += 4) {
+        const int chunk = (half * (D / 8) + t / 4) ^ swz;
+        const float4 kv = *reinterpret_cast<const float4*>(krow + chunk * 4);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[t], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[t + 1], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[t + 2], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[t + 3], s, 0, 0, 0);
+    }
+    return s;
+}
+
+// The workgroup walks its key tiles double-buffered in LDS, each tile loaded
+// straight from global memory into LDS (no register staging), which keeps
+// the kernel within 256 registers: two waves per SIMD, one from each of the
+// two workgroups a CU holds, overlap each other's MFMA and softmax phases.
 template <int D, int VD>
-__global__ __launch_bounds__(256, (D > 64 ? 1 : 2)) void attn_prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
     apply_advance(a);
     using Cfg = PrefillCfg<D, VD>;
     extern __shared__ float lds[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int l32 = lane & 31, half = lane >> 5;
 
     // Heaviest (latest) query tiles first: under a causal mask they see the most keys.
@@ -140,19 +191,28 @@ __global__ __launch_bounds__(256, (D > 64 ? 1 : 2)) void attn_prefill_kernel(Att
     uint64_t q_lo = 0, q_hi = 0;
     if (q_live) key_range(a, a.offset + q, &q_lo, &q_hi);
 
-    // Key range of the whole workgroup and of this wave (for skipping tiles).
+    // Key range of the whole workgroup and of this wave (for skipping tiles),
+    // and the keys every live query of the wave admits (tiles inside need no mask).
     const uint64_t q_last = min(a.seq, q_first + Cfg::kBQ) - 1;
     uint64_t blk_lo, blk_hi, tmp;
     key_range(a, a.offset + q_first, &blk_lo, &tmp);
     key_range(a, a.offset + q_last, &tmp, &blk_hi);
     const uint64_t w_first = q_first + wave * 32;
     const uint64_t w_last = min(a.seq, w_first + 32);
-    uint64_t wave_lo = 0, wave_hi = 0;
+    uint64_t wave_lo = 0, wave_hi = 0, all_lo = 0, all_hi = 0;
     if (w_first < a.seq) {
-        key_range(a, a.offset + w_first, &wave_lo, &tmp);
-        key_range(a, a.offset + w_last - 1, &tmp, &wave_hi);
+        key_range(a, a.offset + w_first, &wave_lo, &all_hi);
+        key_range(a, a.offset + w_last - 1, &all_lo, &wave_hi);
     }
     const uint64_t tile_begin = blk_lo / Cfg::kBKV * Cfg::kBKV;
+    const int ntiles = blk_hi > tile_begin
+                           ? static_cast<int>((blk_hi - tile_begin + Cfg::kBKV - 1) / Cfg::kBKV)
+                           : 0;
+    auto wave_in = [&](uint64_t k0) { return k0 < wave_hi && k0 + Cfg::kBKV > wave_lo; };
+    // This query's admitted keys relative to the first tile (32-bit: the
+    // caller keeps key counts below 2^31).
+    const int rel_lo = static_cast<int>(q_lo > tile_begin ? q_lo - tile_begin : 0);
+    const int rel_hi = static_cast<int>(q_hi > tile_begin ? q_hi - tile_begin : 0);
 
     float m = -INFINITY, l = 0.0f;
     v16f o[VD / 32];
@@ -161,112 +221,85 @@ __global__ __launch_bounds__(256, (D > 64 ? 1 : 2)) void attn_prefill_kernel(Att
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[vb][r] = 0.0f;
 
-    float4 rk[Cfg::kKChunks], rv[Cfg::kVChunks];
-    auto load = [&](uint64_t k0) {
-#pragma unroll
-        for (int i = 0; i < Cfg::kKChunks; ++i) {
-            const int c = threadIdx.x + i * 256;
-            const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-            const uint64_t key = k0 + row;
-            rk[i] = key < a.kv_seq ? *reinterpret_cast<const float4*>(K + key * k_ld + col)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < Cfg::kVChunks; ++i) {
-            const int c = threadIdx.x + i * 256;
-            const int row = c / (VD / 4), col = (c % (VD / 4)) * 4;
-            const uint64_t key = k0 + row;
-            rv[i] = key < a.kv_seq ? *reinterpret_cast<const float4*>(V + key * v_ld + col)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto store = [&](int buf) {
-        float* sk = lds + buf * Cfg::kTile;
-        float* sv = sk + Cfg::kBKV * Cfg::kSK;
-#pragma unroll
-        for (int i = 0; i < Cfg::kKChunks; ++i) {
-            const int c = threadIdx.x + i * 256;
-            *reinterpret_cast<float4*>(sk + (c / (D / 4)) * Cfg::kSK + (c % (D / 4)) * 4) = rk[i];
-        }
-#pragma unroll
-        for (int i = 0; i < Cfg::kVChunks; ++i) {
-            const int c = threadIdx.x + i * 256;
-            *reinterpret_cast<float4*>(sv + (c / (VD / 4)) * Cfg::kSV + (c % (VD / 4)) * 4) = rv[i];
-        }
-    };
+    float* const kbuf0 = lds;
+    float* const vbuf0 = lds + 2 * Cfg::kKTile;
+    auto kbuf = [&](int i) { return kbuf0 + (i & 1) * Cfg::kKTile; };
+    auto vbuf = [&](int i) { return vbuf0 + (i & 1) * Cfg::kVTile; };
+    auto load_k = [&](uint64_t k0, float* dst) { dma_tile<D>(K, k_ld, k0, a.kv_seq, dst, wave, lane); };
+    auto load_v = [&](uint64_t k0, float* dst) { dma_tile<VD>(V, v_ld, k0, a.kv_seq, dst, wave, lane); };
 
-    if (tile_begin < blk_hi) {
-        load(tile_begin);
-        store(0);
+    // V reads: key row `key`, column vb*32 + l32 sits in chunk
+    // (vb*8 + l32/4) ^ (key & 7); key & 7 = 4*half + t%4 for step t.
+    int vx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vx[j] = (((l32 >> 2) ^ (4 * half + j)) << 2) + (l32 & 3);
+
+    // Tile i sits in buffer i & 1 (K and V); tile i+1 is loaded straight into
+    // the other buffer while tile i is used (that buffer held tile i-1, whose
+    // readers all passed the previous barrier).
+    if (ntiles > 0) {
+        load_k(tile_begin, kbuf(0));
+        load_v(tile_begin, vbuf(0));
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    int buf = 0;
-    for (uint64_t k0 = tile_begin; k0 < blk_hi; k0 += Cfg::kBKV, buf ^= 1) {
-        const bool more = k0 + Cfg::kBKV < blk_hi;
-        if (more) load(k0 + Cfg::kBKV);
-        if (k0 < wave_hi && k0 + Cfg::kBKV > wave_lo) {
-            const float* sk = lds + buf * Cfg::kTile;
-            const float* sv = sk + Cfg::kBKV * Cfg::kSK;
-            // S^T[key][query] for the tile: A = K rows (lane -> key l32), B = Q^T.
-            v16f s;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-            const float* krow = sk + l32 * Cfg::kSK + half * (D / 2);
-#pragma unroll
-            for (int t = 0; t < D / 2; t += 4) {
-                const float4 kv = *reinterpret_cast<const float4*>(krow + t);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[t], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[t + 1], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[t + 2], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[t + 3], s, 0, 0, 0);
-            }
-            // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q.
+    for (int i = 0; i < ntiles; ++i) {
+        const uint64_t k0 = tile_begin + static_cast<uint64_t>(i) * Cfg::kBKV;
+        if (i + 1 < ntiles) {
+            load_k(k0 + Cfg::kBKV, kbuf(i + 1));
+            load_v(k0 + Cfg::kBKV, vbuf(i + 1));
+        }
+        if (wave_in(k0)) {
+            v16f s_cur = tile_scores<D>(kbuf(i), qf, l32, half);
+            // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q; bit
+            // j of `admit` says whether tile key j is admitted.
+            const int lo_r = min(max(rel_lo - i * Cfg::kBKV, 0), Cfg::kBKV);
+            const int hi_r = min(max(rel_hi - i * Cfg::kBKV, 0), Cfg::kBKV);
+            const uint64_t span = ((1ull << hi_r) - 1ull) & ~((1ull << lo_r) - 1ull);
+            const uint32_t mine = static_cast<uint32_t>(span) >> (4 * half);
             float tile_max = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint64_t key = k0 + 8 * (r / 4) + 4 * half + (r % 4);
-                const bool ok = q_live && key >= q_lo && key < q_hi;
-                s[r] = ok ? s[r] : -INFINITY;
-                tile_max = fmaxf(tile_max, s[r]);
+                const int key = 8 * (r / 4) + (r % 4);
+                s_cur[r] = (mine >> key) & 1u ? s_cur[r] : -INFINITY;
+                tile_max = fmaxf(tile_max, s_cur[r]);
             }
             tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
             // Every lane runs the update (the MFMAs below need the whole wave);
             // a query with no admitted key yet keeps m = -inf, l = 0, o = 0.
             const float m_new = fmaxf(m, tile_max);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = exp2f(m - m_use);
+            const float alpha = __builtin_amdgcn_exp2f(m - m_use);
             float psum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[r] = exp2f(s[r] - m_use);
-                psum += s[r];
+                s_cur[r] = __builtin_amdgcn_exp2f(s_cur[r] - m_use);
+                psum += s_cur[r];
             }
             psum += __shfl_xor(psum, 32, 64);
             const float l_new = l * alpha + psum;
-            const float inv = l_new > 0.0f ? 1.0f / l_new : 0.0f;
+            const float inv = l_new > 0.0f ? __builtin_amdgcn_rcpf(l_new) : 0.0f;
             // A tile that adds nothing for this query leaves its output as it was.
             const float keep = (psum == 0.0f && alpha == 1.0f) || l_new == 0.0f ? 1.0f : (l * alpha) * inv;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] *= inv;
-#pragma unroll
-            for (int vb = 0; vb < VD / 32; ++vb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[vb][r] *= keep;
-            // O^T += V^T . P^T: step t pairs key 8*(t/4) + 4*half + t%4 with register t.
+            for (int r = 0; r < 16; ++r) s_cur[r] *= inv;
+            const float* sv = vbuf(i);
 #pragma unroll
             for (int vb = 0; vb < VD / 32; ++vb) {
-                const float* vcol = sv + vb * 32 + l32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[vb][r] *= keep;
+                // O^T += V^T . P^T: step t pairs key 8*(t/4) + 4*half + t%4 with register t.
 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
-                    const int key = 8 * (t / 4) + 4 * half + (t % 4);
-                    o[vb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vcol[key * Cfg::kSV], s[t],
-                                                                o[vb], 0, 0, 0);
+                    const int key_row = 8 * (t / 4) + 4 * half + (t % 4);
+                    const float v = sv[key_row * VD + vb * 32 + vx[t % 4]];
+                    o[vb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, s_cur[t], o[vb], 0, 0, 0);
                 }
             }
             m = m_new;
             l = l_new;
         }
-        if (more) store(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
@@ -743,8 +776,9 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
         }
         if (st != MHIP_CAPTURE_UNSUPPORTED) return st;  // else: no decode kernel for this d
     }
-    if (aligned && vd == d && d == 128) return launch_prefill<128, 128>(ctx, a, batch);
-    if (aligned && vd == d && d == 64) return launch_prefill<64, 64>(ctx, a, batch);
+    const bool small_keys = p->kv_rows < (1ULL << 31);  // the MFMA kernel's key arithmetic is 32-bit
+    if (aligned && small_keys && vd == d && d == 128) return launch_prefill<128, 128>(ctx, a, batch);
+    if (aligned && small_keys && vd == d && d == 64) return launch_prefill<64, 64>(ctx, a, batch);
     if (vd > 256) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention value dimension above 256");
     const uint64_t total = batch * p->seq_len * H;
     if (total / 4 >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention: too many rows");
