@@ -308,7 +308,9 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (tiles >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: too many tiles");
-    const uint64_t slots = 2ULL * (ctx->compute_units ? ctx->compute_units : 256);
+    // Resident workgroups per CU: as many tiles as fit the 160 KB of LDS.
+    const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
+    const uint64_t slots = per_cu * (ctx->compute_units ? ctx->compute_units : 256);
     uint64_t k_split = k;
     const uint64_t splits = choose_splits(tiles, k, slots, BK, &k_split);
     float* target = c;
@@ -733,6 +735,12 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         return dispatch_gemv<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
+    // Big products (enough 256 x 256 tiles to give every CU one): 8 waves of
+    // 64 x 128 per tile, twice the MFMA work per byte of LDS traffic.
+    const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
+    const bool big = ((m + 255) / 256) * ((n + 255) / 256) >= cus;
+    if (!ta && !tb && big)
+        return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (!ta && !tb)
         return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (ta && !tb)

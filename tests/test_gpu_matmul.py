@@ -131,3 +131,28 @@ def test_square_baseline_sizes(dev, orc, size):
     err = np.max(np.abs(lhs - rhs)) / np.max(np.abs(rhs))
     print(f"matmul {size}^3 checksum err {err:.2e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("m,k,n,mode", [(4100, 64, 4100, 0), (4096, 96, 4164, 1), (4164, 40, 4096, 2)])
+def test_large_tile_path_ragged_edges_and_addends(dev, orc, m, k, n, mode):
+    """Products with at least one 256 x 256 tile per CU take the 8-wave tile
+    kernel; ragged edges and both addend forms against the oracle, and the
+    fused addend bit-identical to matmul + add."""
+    from magnetar_hip import ops
+    a = orc.uniform(m * k, 31 + m, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 32 + n, -1.0, 1.0).reshape(k, n)
+    addend = None
+    if mode == 1:
+        addend = orc.uniform(n, 33, -1.0, 1.0)
+    elif mode == 2:
+        addend = orc.uniform(m * n, 34, -1.0, 1.0).reshape(m, n)
+    da, db = dev.upload(a), dev.upload(b)
+    dadd = dev.upload(addend) if addend is not None else None
+    got = ops.matmul(dev, da, db, addend=dadd, addend_mode=mode).numpy()
+    want, st = orc.matmul(a, b, addend=addend, addend_mode=mode)
+    assert st == 0
+    assert max_normwise_err(got, want) <= 1e-4
+    if mode:
+        plain = ops.matmul(dev, da, db)
+        summed = (ops.add(dev, plain, dadd) if mode == 2 else ops.bias_add(dev, plain, dadd)).numpy()
+        assert np.array_equal(got.view(np.uint32), summed.view(np.uint32))
