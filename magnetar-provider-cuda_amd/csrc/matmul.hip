@@ -302,6 +302,26 @@ uint64_t choose_splits(uint64_t tiles, uint64_t k, uint64_t slots, uint64_t bk,
     return (k + per - 1) / per;
 }
 
+// Estimated seconds for an m x k x n product with one tile configuration:
+// rounds of resident workgroups times each one's share of the MFMA work (at
+// the configuration's measured fraction of peak, shared by the workgroups a
+// CU holds), plus the split-k reduce's traffic. Picks between the 128 x 128
+// and 256 x 256 kernels.
+double gemm_seconds(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n, uint64_t bm,
+                    uint64_t bn, uint64_t bk, uint64_t lds_bytes, double efficiency) {
+    const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
+    const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / lds_bytes);
+    const uint64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    uint64_t k_split = k;
+    const uint64_t splits = choose_splits(tiles, k, per_cu * cus, bk, &k_split);
+    const uint64_t rounds = (tiles * splits + per_cu * cus - 1) / (per_cu * cus);
+    const double cu_flops = 157.3e12 / 256.0;  // dense fp32 MFMA per CU per second
+    const double slot_flops = cu_flops * efficiency / static_cast<double>(per_cu);
+    double t = static_cast<double>(rounds) * 2.0 * bm * bn * k_split / slot_flops;
+    if (splits > 1) t += static_cast<double>(splits + 1) * m * n * 4.0 / 5.0e12;
+    return t;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT>
 mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
                         uint64_t k, uint64_t n, const float* addend, int mode, bool vec) {
@@ -735,11 +755,15 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         return dispatch_gemv<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
-    // Big products (enough 256 x 256 tiles to give every CU one): 8 waves of
-    // 64 x 128 per tile, twice the MFMA work per byte of LDS traffic.
-    const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
-    const bool big = ((m + 255) / 256) * ((n + 255) / 256) >= cus;
-    if (!ta && !tb && big)
+    // 256 x 256 tiles (8 waves of 64 x 128: twice the MFMA work per byte of
+    // LDS traffic, measured at ~81 % of peak against ~70 % for 128 x 128)
+    // wherever the model expects them to finish first, split-k included.
+    using Big = TileCfg<256, 256, 32, 64, 128, false, false>;
+    using Small = TileCfg<128, 128, 32, 64, 64, false, false>;
+    const bool big = !ta && !tb &&
+                     gemm_seconds(ctx, m, k, n, 256, 256, 32, Big::kLdsFloats * sizeof(float), 0.81) <
+                         gemm_seconds(ctx, m, k, n, 128, 128, 32, Small::kLdsFloats * sizeof(float), 0.70);
+    if (big)
         return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (!ta && !tb)
         return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
