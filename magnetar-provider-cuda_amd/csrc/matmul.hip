@@ -21,7 +21,8 @@
 //    gives 128 tiles of 128 x 128 for 256 CUs), k is split over up to 8
 //    workgroups per tile; their partial tiles go to a workspace and a second
 //    launch adds them in split order (deterministic) with the addend.
-//  - m <= kGemvMaxRows (decode): the work is reading B once (HBM-bound), so
+//  - m <= kGemvMaxRows (decode), or up to 32 rows of a small product in row
+//    blocks of 8: the work is reading B once (HBM-bound), so
 //    each wave streams 256 columns of B with dwordx4 loads over one k slice,
 //    keeping m x 4 partial sums per lane; partial sums per k slice go to a
 //    workspace and a second launch adds them in a fixed order
@@ -456,11 +457,18 @@ __device__ __forceinline__ void gemv_partial_body(
     }
 }
 
+// blockIdx.z is a block of ROWS rows of A and C: each is an independent
+// ROWS-row GEMV with its own partial sums (B is shared through L2).
 template <int ROWS, class BT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
     const float* __restrict__ addend, int addend_mode) {
+    const uint64_t rb = blockIdx.z;
+    A += rb * ROWS * K;
+    C += rb * ROWS * N;
+    if (partial) partial += rb * slices * ROWS * N;
+    if (addend_mode == 2) addend += rb * ROWS * N;
     gemv_partial_body<ROWS, BT>(A, B, partial, C, K, N, k_per_slice, blockIdx.x, blockIdx.y,
                             slices == 1, addend, addend_mode);
 }
@@ -519,6 +527,10 @@ template <int ROWS>
 __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     const float* __restrict__ partial, float* __restrict__ C, uint64_t N, uint32_t slices,
     const float* __restrict__ addend, int addend_mode) {
+    const uint64_t rb = blockIdx.z;  // row block, as in gemv_partial_kernel
+    partial += rb * slices * ROWS * N;
+    C += rb * ROWS * N;
+    if (addend_mode == 2) addend += rb * ROWS * N;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
     const bool live = col < N;
@@ -667,22 +679,24 @@ void gemv_slicing(const mhip_ctx* ctx, uint64_t k, uint64_t n, uint64_t* slices_
 
 template <int ROWS, class BT>
 mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t k,
-                        uint64_t n, const float* addend, int mode) {
+                        uint64_t n, const float* addend, int mode, uint64_t row_blocks = 1) {
     const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
     uint64_t slices, k_per_slice;
     gemv_slicing(ctx, k, n, &slices, &k_per_slice);
     float* partial = nullptr;
     if (slices > 1) {
-        mhip_status st = workspace(ctx, slices * ROWS * n * sizeof(float), &partial);
+        mhip_status st = workspace(ctx, row_blocks * slices * ROWS * n * sizeof(float), &partial);
         if (st != MHIP_OK) return st;
     }
     hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT>),
-                       dim3(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices)),
+                       dim3(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices),
+                            static_cast<unsigned>(row_blocks)),
                        dim3(kGemvThreads), 0, ctx->stream, a, b, partial, c, k, n, k_per_slice,
                        static_cast<uint32_t>(slices), addend, mode);
     mhip_status st = mhip::check_launch("matmul (decode partial sums)");
     if (st != MHIP_OK || slices == 1) return st;
-    hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>, dim3(static_cast<unsigned>(col_groups)),
+    hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>,
+                       dim3(static_cast<unsigned>(col_groups), 1, static_cast<unsigned>(row_blocks)),
                        dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
                        static_cast<uint32_t>(slices), addend, mode);
     return mhip::check_launch("matmul (decode reduction)");
@@ -753,6 +767,12 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
     const bool b_aligned = (reinterpret_cast<uintptr_t>(b) & b_align) == 0;
     if (m <= kGemvMaxRows && !ta && !tb && n % 4 == 0 && b_aligned)
         return dispatch_gemv<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
+    // A few rows of a small product (up to 32 rows in blocks of 8, at most
+    // 2^26 multiply-adds): the GEMV's two short launches beat MFMA tiles that
+    // would be three quarters padding and walk k serially.
+    if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= (1ull << 26) && !ta && !tb &&
+        n % 4 == 0 && b_aligned)
+        return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
     // 256 x 256 tiles (8 waves of 64 x 128: twice the MFMA work per byte of

@@ -156,3 +156,34 @@ def test_large_tile_path_ragged_edges_and_addends(dev, orc, m, k, n, mode):
         plain = ops.matmul(dev, da, db)
         summed = (ops.add(dev, plain, dadd) if mode == 2 else ops.bias_add(dev, plain, dadd)).numpy()
         assert np.array_equal(got.view(np.uint32), summed.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n,mode", [(16, 256, 256, 0), (24, 688, 256, 1), (32, 256, 688, 2),
+                                        (32, 100, 300, 0), (16, 4096, 1024, 2)])
+def test_row_blocked_gemv(dev, orc, m, k, n, mode):
+    """Small products of 16-32 rows run as blocks of 8 rows on the split-k
+    GEMV: against the oracle, and each block of 8 rows bit-identical to the
+    8-row GEMV of those rows alone (same slicing of k, same summation order)."""
+    from magnetar_hip import ops
+    a = orc.uniform(m * k, 41 + m, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 42 + n, -1.0, 1.0).reshape(k, n)
+    addend = None
+    if mode == 1:
+        addend = orc.uniform(n, 43, -1.0, 1.0)
+    elif mode == 2:
+        addend = orc.uniform(m * n, 44, -1.0, 1.0).reshape(m, n)
+    db = dev.upload(b)
+    got = ops.matmul(dev, dev.upload(a), db, addend=dev.upload(addend) if addend is not None else None,
+                     addend_mode=mode).numpy()
+    want, st = orc.matmul(a, b, addend=addend, addend_mode=mode)
+    assert st == 0
+    assert max_normwise_err(got, want) <= TOL
+    for r in range(0, m, 8):
+        part = None
+        if mode == 1:
+            part = dev.upload(addend)
+        elif mode == 2:
+            part = dev.upload(np.ascontiguousarray(addend[r:r + 8]))
+        block = ops.matmul(dev, dev.upload(np.ascontiguousarray(a[r:r + 8])), db, addend=part,
+                           addend_mode=mode).numpy()
+        assert_bitexact(got[r:r + 8], block)
