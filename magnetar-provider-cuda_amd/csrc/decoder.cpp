@@ -11,9 +11,10 @@
 // (`key_count`). Here the K and V projections are written straight into
 // their cache rows and rotated in place, so the append costs no copy, and the
 // residual adds ride in the matmul epilogues (matmul-residual, bit-identical
-// to matmul + add). For decode (up to 8 rows) the Q/K/V and gate/up
-// projections each run as one fused GEMV set whose reduction applies RoPE or
-// silu * up, and the embedding row is normalised as it is gathered; every
+// to matmul + add). For decode (up to 8 rows, or up to 32 in blocks of 8 when
+// the products are small) the Q/K/V and gate/up projections each run as one
+// fused GEMV set whose reduction applies RoPE or silu * up, and the embedding
+// row is normalised as it is gathered; every
 // fusion is bit-identical to the separate calls. All launches go on the
 // context's stream; nothing waits.
 #include <cstring>
@@ -111,7 +112,8 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     rope[0].position_offset = position;
     rope[1] = rope[0];
     rope[1].head_count = c.kv_heads;
-    // Decode (a few rows): Q, K, V as one set of GEMVs with RoPE applied where
+    // Decode (a few rows, or a few blocks of 8 rows of a small block): Q, K, V
+    // as one set of GEMVs with RoPE applied where
     // their split-k sums are added. Otherwise three matmuls and two RoPE calls.
     // In a captured step whose row offset advances, the K/V rows written
     // follow the replay offset (the rows left below them bound it).
@@ -123,7 +125,7 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
         // The separate matmuls write fixed rows of the cache.
         if (mhip::capture_advancing(ctx) & MHIP_ADVANCE_ROW_OFFSET)
-            return mhip::forbid_in_capture(ctx, "a K/V append of more than 8 rows with an advancing row offset");
+            return mhip::forbid_in_capture(ctx, "a K/V append that the fused projections cannot take with an advancing row offset");
         MHIP_TRY(mm(h, w->wq, q, seq, c.hidden, c.heads * c.head_dim, nullptr, 0));
         MHIP_TRY(mm(h, w->wk, k_rows, seq, c.hidden, kv_dim, nullptr, 0));
         MHIP_TRY(mm(h, w->wv, v_rows, seq, c.hidden, kv_dim, nullptr, 0));
@@ -148,7 +150,7 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
     MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
     MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
-    // Decode: gate and up as one set of GEMVs whose reduction writes
+    // Decode (as for Q/K/V): gate and up as one set of GEMVs whose reduction writes
     // silu(gate) * up. Otherwise two matmuls and silu-mul.
     const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};
     st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr, bf16);

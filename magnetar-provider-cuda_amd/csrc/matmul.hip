@@ -35,6 +35,9 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kGemvMaxRows = 8;
+// Largest product (m x k x n multiply-adds) that 16-32 rows run on the GEMV
+// in row blocks rather than on MFMA tiles.
+constexpr uint64_t kGemvSmallProduct = 1ull << 26;
 
 // Split-k partial sums live in the context's workspace; stream order makes
 // reuse by the next call safe.
@@ -596,7 +599,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const fl
                   : (set.count > 1 && b >= set.seg[1].first_block) ? 1 : 0;
     const GemvSeg s = pick(set, i);
     const uint32_t local = b - s.first_block;
-    gemv_partial_body<ROWS, BT>(A, static_cast<const BT*>(s.b), s.partial, nullptr, K, s.n, s.k_per_slice,
+    const uint64_t rb = blockIdx.y;  // row block of ROWS rows
+    gemv_partial_body<ROWS, BT>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
+                            s.partial + rb * s.slices * ROWS * s.n, nullptr, K, s.n, s.k_per_slice,
                             local % s.col_groups, local / s.col_groups, false, nullptr, 0);
 }
 
@@ -623,19 +628,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
     const int i = (set.count > 2 && b >= set.seg[2].first_group) ? 2
                   : (set.count > 1 && b >= set.seg[1].first_group) ? 1 : 0;
     const GemvSeg s = pick(set, i);
+    const uint64_t rb = blockIdx.y;  // row block, as in gemv_set_partial_kernel
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(b - s.first_group) * kGemvCols + lane * 4;
     const bool live = col < s.n;
     float4 v[ROWS];
-    gemv_reduce_sum<ROWS>(s.partial, s.n, s.slices, col, live, v);
+    gemv_reduce_sum<ROWS>(s.partial + rb * s.slices * ROWS * s.n, s.n, s.slices, col, live, v);
     if (epilogue == mhip::kGemvSiluMul) {
         // Up projection: the same columns of segment 1.
         const GemvSeg u = pick(set, 1);
         float4 w[ROWS];
         __syncthreads();
-        gemv_reduce_sum<ROWS>(u.partial, u.n, u.slices, col, live, w);
+        gemv_reduce_sum<ROWS>(u.partial + rb * u.slices * ROWS * u.n, u.n, u.slices, col, live, w);
         if (wave != 0 || !live) return;
-        float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0);
+        float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0) + rb * ROWS * s.n;
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             float4 o;
@@ -648,11 +654,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
         return;
     }
     if (wave != 0 || !live) return;
-    float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0);
+    float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0) + rb * ROWS * s.n;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         float4 o = v[r];
-        if (epilogue == mhip::kGemvRopeQK && i < 2) o = rope_vec(i == 0 ? rope_q : rope_k, r, col, o);
+        if (epilogue == mhip::kGemvRopeQK && i < 2)
+            o = rope_vec(i == 0 ? rope_q : rope_k, rb * ROWS + r, col, o);
         *reinterpret_cast<float4*>(out + r * s.n + col) = o;
     }
 }
@@ -704,15 +711,16 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
 
 template <int ROWS, class BT>
 mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
-                            const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups) {
+                            const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups,
+                            uint32_t row_blocks = 1) {
     uint32_t blocks = 0;
     for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
-    hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT>), dim3(blocks), dim3(kGemvThreads), 0,
-                       ctx->stream, a, k, set);
+    hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT>), dim3(blocks, row_blocks),
+                       dim3(kGemvThreads), 0, ctx->stream, a, k, set);
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
-    hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups), dim3(kGemvThreads), 0,
-                       ctx->stream, set, epilogue, rq, rk);
+    hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups, row_blocks),
+                       dim3(kGemvThreads), 0, ctx->stream, set, epilogue, rq, rk);
     return mhip::check_launch("decode projections (reduction)");
 }
 
@@ -770,7 +778,7 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
     // A few rows of a small product (up to 32 rows in blocks of 8, at most
     // 2^26 multiply-adds): the GEMV's two short launches beat MFMA tiles that
     // would be three quarters padding and walk k serially.
-    if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= (1ull << 26) && !ta && !tb &&
+    if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= kGemvSmallProduct && !ta && !tb &&
         n % 4 == 0 && b_aligned)
         return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
@@ -824,7 +832,9 @@ mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint
         case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g);
         case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g);
         case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        default: return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        default:
+            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g,
+                                          static_cast<uint32_t>(rows / kGemvMaxRows));
     }
 }
 
@@ -836,8 +846,14 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
                          const GemvTarget* targets, int count, int epilogue,
                          const mhip_rope_params* rope, bool bf16_weights) {
     MHIP_REQUIRE_CTX(ctx);
-    if (!a || !targets || count < 1 || count > 3 || rows == 0 || rows > kGemvMaxRows || k == 0)
-        return MHIP_LAYOUT_UNSUPPORTED;
+    if (!a || !targets || count < 1 || count > 3 || rows == 0 || k == 0) return MHIP_LAYOUT_UNSUPPORTED;
+    // Up to 8 rows, or up to 32 in blocks of 8 when every product is small
+    // (as for the row-blocked matmul).
+    if (rows > kGemvMaxRows) {
+        if (rows > 4 * kGemvMaxRows || rows % kGemvMaxRows != 0) return MHIP_LAYOUT_UNSUPPORTED;
+        for (int i = 0; i < count; ++i)
+            if (rows * k * targets[i].n > kGemvSmallProduct) return MHIP_LAYOUT_UNSUPPORTED;
+    }
     if (epilogue == kGemvSiluMul && (count != 2 || targets[0].n != targets[1].n))
         return MHIP_LAYOUT_UNSUPPORTED;
     if (epilogue == kGemvRopeQK && (count < 2 || !rope)) return MHIP_LAYOUT_UNSUPPORTED;

@@ -134,16 +134,19 @@ def unfused_block(dev, s, w, ids, position, k_cache, v_cache):
     return ops.matmul(dev, f, w["w_down"], addend=x2, addend_mode=2)
 
 
-@pytest.mark.parametrize("seq,position", [(1, 40), (3, 20), (8, 0), (32, 0)])
+@pytest.mark.parametrize("seq,position", [(1, 40), (3, 20), (8, 0), (16, 8), (24, 0), (32, 0),
+                                          (20, 4), (40, 0)])
 def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, position):
     """The decode fusions (embedding + rmsnorm, Q/K/V GEMVs with RoPE in the
     reduction, gate/up GEMVs with silu * up) change launches, not arithmetic:
-    the block output and the cache rows equal the unfused chain's bit for bit."""
+    the block output and the cache rows equal the unfused chain's bit for bit.
+    16-32 rows take the sets in row blocks of 8; 20 and 40 rows take the
+    separate calls in the block too."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
     s = Shapes(vocab=1024, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1376)
     w = weights_for(orc, s, 500)
     rows = 64
-    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=32)
+    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=40)
     kc = orc.normal(rows * 128, 501, 0.0, 0.5).reshape(rows, 128)
     vc = orc.normal(rows * 128, 502, 0.0, 0.5).reshape(rows, 128)
     block.k_cache = dev.upload(kc)
