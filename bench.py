@@ -275,22 +275,68 @@ def decoder_cases(dev, orc):
     return cases
 
 
-def cpu_baseline(orc, budget_s=12.0):
-    """The oracle's matmul (f32, k ascending, one thread) on whole rows of the
-    4096^3 headline product, as many rows as fit the time budget."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _host_threads() -> int:
+    """Threads this process may use: its CPU affinity, capped by
+    OMP_NUM_THREADS where the host sets a share."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() and int(cap) > 0 else n
+
+
+def cpu_baseline(orc, runs=5, run_s=1.5):
+    """The oracle's matmul (f32, k ascending; oracle/oracle.c orc_matmul_rows)
+    on whole rows of the 4096^3 headline product: median of `runs` timed runs
+    after a warm-up, single-threaded (the reference order) and parallel over
+    rows on every usable host thread (ctypes releases the GIL). Each run
+    covers as many rows as take about `run_s` seconds on one thread."""
+    from concurrent.futures import ThreadPoolExecutor
     size = 4096
     a = orc.uniform(size * size, seed(2, size), -1.0, 1.0).reshape(size, size)
     b = orc.uniform(size * size, seed(2, size + 1), -1.0, 1.0).reshape(size, size)
-    rows, t0 = 0, time.perf_counter()
-    step = 4
-    while time.perf_counter() - t0 < budget_s and rows < size:
-        orc.matmul_rows(a, b, rows, rows + step)
-        rows += step
-    elapsed = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * size * size / elapsed / 1e12, 6), "unit": "TFLOP/s",
-            "cores": 1, "kind": "port",
-            "sample": f"{rows} of {size} rows of the {size}^3 f32 product ({elapsed:.1f} s, "
-                      f"oracle/oracle.c orc_matmul_rows, one thread)"}
+    t0 = time.perf_counter()
+    orc.matmul_rows(a, b, 0, 2)  # warm-up, and the per-row time
+    per_row = (time.perf_counter() - t0) / 2
+    rows = int(min(size, max(2, run_s / max(per_row, 1e-6))))
+    flop_per_row = 2.0 * size * size
+
+    def timed(fn):
+        times = []
+        for _ in range(runs):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times))
+
+    single = timed(lambda: orc.matmul_rows(a, b, 0, rows))
+    threads = _host_threads()
+    par_rows = min(size, rows * threads)
+    bounds = np.linspace(0, par_rows, threads + 1).astype(int)
+    with ThreadPoolExecutor(threads) as pool:
+        def parallel():
+            list(pool.map(lambda i: orc.matmul_rows(a, b, int(bounds[i]), int(bounds[i + 1])),
+                          range(threads)))
+        parallel()  # warm-up
+        par = timed(parallel)
+    single_tflops = flop_per_row * rows / single / 1e12
+    return {"value": round(flop_per_row * par_rows / par / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{par_rows} of {size} rows of the {size}^3 f32 product split over {threads} "
+                      f"threads, median of {runs} runs ({par:.2f} s each) after a warm-up "
+                      f"(oracle/oracle.c orc_matmul_rows)",
+            "single_thread": {"value": round(single_tflops, 6), "cores": 1,
+                              "sample": f"{rows} rows, median of {runs} runs ({single:.2f} s each)"},
+            "cpu_model": _cpu_model(), "nproc": os.cpu_count()}
 
 
 def _reshape(arr, shape):
