@@ -14,8 +14,8 @@
 // Three kernels:
 //  - prefill (head dims 64 and 128): fp32 MFMA flash attention. A workgroup
 //    takes 128 queries of one (batch, head), four waves of 32, and walks the
-//    admitted keys in 32-key tiles staged in LDS (double-buffered through
-//    registers). Each wave computes S^T = K . Q^T with v_mfma_f32_32x32x2_f32
+//    admitted keys in 32-key tiles loaded straight into LDS (direct
+//    global -> LDS loads, XOR-swizzled, double-buffered). Each wave computes S^T = K . Q^T with v_mfma_f32_32x32x2_f32
 //    (Q^T lives in registers, pre-scaled by scale * log2 e), so every lane
 //    owns one query column and 16 of the tile's keys: the online-softmax
 //    max/sum need one exchange with lane l ^ 32. The accumulator registers
