@@ -159,11 +159,17 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int l32 = lane & 31, half = lane >> 5;
 
-    // Heaviest (latest) query tiles first: under a causal mask they see the most keys.
+    // Heaviest (latest) query tiles first over the whole grid: under a causal
+    // mask they see the most keys. Block ids are dealt round-robin to the 8
+    // XCDs, so consecutive ids take the same query tile of different (batch,
+    // head) pairs: every XCD gets an equal share of each weight class and runs
+    // it heaviest first (ids of one head's query tiles, dealt to XCDs by
+    // query tile, left XCDs with 2.4x the work of others).
     const uint64_t qtiles = (a.seq + Cfg::kBQ - 1) / Cfg::kBQ;
+    const uint64_t pairs = gridDim.x / qtiles;
     const uint64_t bid = blockIdx.x;
-    const uint64_t qt = qtiles - 1 - bid % qtiles;
-    const uint64_t bh = bid / qtiles;
+    const uint64_t qt = qtiles - 1 - bid / pairs;
+    const uint64_t bh = bid % pairs;
     const uint64_t head = bh % a.heads, b = bh / a.heads;
     const uint64_t kvh = head / (a.heads / a.kv_heads);
 
