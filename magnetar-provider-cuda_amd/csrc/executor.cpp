@@ -578,7 +578,9 @@ struct mhip_executor {
     }
 
     // gated-matmul: silu(a . gate) * (a . up), as the two matmuls and
-    // silu-mul it fuses (src/executor.rs:1484-1494).
+    // silu-mul it fuses (src/executor.rs:1484-1494). A few rows (decode) run
+    // as one GEMV set whose reduction writes silu(gate) * up: no temporaries,
+    // bit-identical to the two matmuls and silu-mul.
     BufferPtr op_gated_matmul(const Invocation& inv, BufferPtr& offered) {
         const Buffer& a = get(inv, 0);
         const Buffer& gate = get(inv, 1);
@@ -596,6 +598,15 @@ struct mhip_executor {
         require_f32(a, "gated-matmul");
         require_f32(gate, "gated-matmul");
         require_f32(up, "gated-matmul");
+        if (!ta && !tb && gate.compact == up.compact && m > 0 && n > 0 && k > 0) {
+            BufferPtr out = alloc_output(offered, Shape{m, n}, MHIP_DTYPE_F32);
+            const mhip::GemvTarget t[2] = {{gate.ptr, n, out->f()}, {up.ptr, n, nullptr}};
+            const mhip_status st =
+                mhip::gemv_set_f32(ctx, a.f(), m, k, t, 2, mhip::kGemvSiluMul, nullptr, gate.compact);
+            if (st == MHIP_OK) return out;
+            if (st != MHIP_LAYOUT_UNSUPPORTED) check(st);
+            offered = std::move(out);  // reused below
+        }
         Buffer g(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
         Buffer u(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
         check(matmul(a, gate, g.f(), m, k, n, ta, tb, nullptr, 0));

@@ -384,8 +384,11 @@ constexpr int kGemvCols = 256;  // columns per workgroup: 64 lanes x 4
 // One workgroup's share of a decode GEMV: column group `cg` (256 columns)
 // and k slice `slice`. Its 4 waves split the slice's rows and meet in LDS.
 // `direct`: write C (+ addend) itself (the only slice); otherwise write the
-// slice's partial sums for the reduction.
-template <int ROWS, class BT>
+// slice's partial sums for the reduction. STREAM: read B non-temporally (a
+// matrix larger than an XCD's L2, read once per call); a small B is read
+// through the caches, where it stays between calls. (A template parameter:
+// a run-time choice inside the load loop doubled the registers.)
+template <int ROWS, class BT, bool STREAM>
 __device__ __forceinline__ void gemv_partial_body(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t cg,
@@ -407,8 +410,10 @@ __device__ __forceinline__ void gemv_partial_body(
         for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
             float4 bv[kU];
 #pragma unroll
-            for (int u = 0; u < kU; ++u)
-                bv[u] = load4_nt(B + (kk + 4 * u) * N + col);
+            for (int u = 0; u < kU; ++u) {
+                if constexpr (STREAM) bv[u] = load4_nt(B + (kk + 4 * u) * N + col);
+                else bv[u] = load4(B + (kk + 4 * u) * N + col);
+            }
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
 #pragma unroll
@@ -422,7 +427,9 @@ __device__ __forceinline__ void gemv_partial_body(
             }
         }
         for (; kk < k_end; kk += 4) {
-            const float4 bv = load4_nt(B + kk * N + col);
+            float4 bv;
+            if constexpr (STREAM) bv = load4_nt(B + kk * N + col);
+            else bv = load4(B + kk * N + col);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const float a = A[r * K + kk];
@@ -462,7 +469,7 @@ __device__ __forceinline__ void gemv_partial_body(
 
 // blockIdx.z is a block of ROWS rows of A and C: each is an independent
 // ROWS-row GEMV with its own partial sums (B is shared through L2).
-template <int ROWS, class BT>
+template <int ROWS, class BT, bool STREAM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
@@ -472,45 +479,51 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     C += rb * ROWS * N;
     if (partial) partial += rb * slices * ROWS * N;
     if (addend_mode == 2) addend += rb * ROWS * N;
-    gemv_partial_body<ROWS, BT>(A, B, partial, C, K, N, k_per_slice, blockIdx.x, blockIdx.y,
-                            slices == 1, addend, addend_mode);
+    gemv_partial_body<ROWS, BT, STREAM>(A, B, partial, C, K, N, k_per_slice, blockIdx.x,
+                                        blockIdx.y, slices == 1, addend, addend_mode);
 }
 
 // Sum of the slices' partial sums of 256 columns: wave w adds a fixed
-// quarter of the slices (eight loads in flight), then wave 0 adds the
-// quarters in order -- the same order on every run. The result is valid in
-// wave 0 only; every thread of the workgroup must call it (it synchronises),
-// and a second call must come after a __syncthreads().
+// quarter of the slices, each row in slice order, then wave 0 adds the
+// quarters in order -- the same order on every run. Loads go out in batches
+// of 16 float4 (all rows of 16 / ROWS slices) before any is added, so a
+// quarter costs ceil(slices / 4 / batch) memory round trips, not one per
+// slice and row. The result is valid in wave 0 only; every thread of the
+// workgroup must call it (it synchronises), and a second call must come
+// after a __syncthreads().
 template <int ROWS>
 __device__ __forceinline__ void gemv_reduce_sum(const float* __restrict__ partial, uint64_t N,
                                                 uint32_t slices, uint64_t col, bool live,
                                                 float4 (&out)[ROWS]) {
     __shared__ float4 red[4][ROWS][64];
+    constexpr int kBatch = ROWS >= 16 ? 1 : 16 / ROWS;  // slices per batch
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t quarter = (slices + 3) / 4;
     const uint32_t s_begin = min(slices, wave * quarter), s_end = min(slices, s_begin + quarter);
+    float4 v[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (live) {
-            uint32_t s = s_begin;
-            for (; s + 7 < s_end; s += 8) {
-                float4 p[8];
+    for (int r = 0; r < ROWS; ++r) v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+        for (uint32_t s = s_begin; s < s_end; s += kBatch) {
+            float4 p[kBatch][ROWS];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    p[u] = *reinterpret_cast<const float4*>(partial + ((s + u) * static_cast<uint64_t>(ROWS) + r) * N + col);
+            for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    v.x += p[u].x; v.y += p[u].y; v.z += p[u].z; v.w += p[u].w;
-                }
-            }
-            for (; s < s_end; ++s) {
-                const float4 p = *reinterpret_cast<const float4*>(partial + (s * static_cast<uint64_t>(ROWS) + r) * N + col);
-                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
-            }
+                for (int r = 0; r < ROWS; ++r)
+                    if (s + u < s_end)
+                        p[u][r] = *reinterpret_cast<const float4*>(
+                            partial + ((s + u) * static_cast<uint64_t>(ROWS) + r) * N + col);
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    if (s + u < s_end) {
+                        v[r].x += p[u][r].x; v[r].y += p[u][r].y; v[r].z += p[u][r].z; v[r].w += p[u][r].w;
+                    }
         }
-        red[wave][r][lane] = v;
     }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) red[wave][r][lane] = v[r];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
@@ -591,7 +604,7 @@ __device__ __forceinline__ GemvSeg pick(const GemvSet& set, int i) {
     return set.seg[2];
 }
 
-template <int ROWS, class BT>
+template <int ROWS, class BT, bool STREAM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const float* __restrict__ A,
                                                                         uint64_t K, GemvSet set) {
     const uint32_t b = blockIdx.x;
@@ -600,9 +613,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const fl
     const GemvSeg s = pick(set, i);
     const uint32_t local = b - s.first_block;
     const uint64_t rb = blockIdx.y;  // row block of ROWS rows
-    gemv_partial_body<ROWS, BT>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
-                            s.partial + rb * s.slices * ROWS * s.n, nullptr, K, s.n, s.k_per_slice,
-                            local % s.col_groups, local / s.col_groups, false, nullptr, 0);
+    gemv_partial_body<ROWS, BT, STREAM>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
+                                        s.partial + rb * s.slices * ROWS * s.n, nullptr, K, s.n,
+                                        s.k_per_slice, local % s.col_groups, local / s.col_groups,
+                                        false, nullptr, 0);
 }
 
 __device__ __forceinline__ float4 rope_vec(const RopeEpi& e, uint64_t row, uint64_t col, float4 v) {
@@ -665,6 +679,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
 }
 
 
+// Whether a GEMV reads its matrix non-temporally: one larger than an XCD's
+// 4 MB L2 is streamed; a smaller one is kept in the caches across calls
+// (the small blocks' weights), which saves a trip to HBM per launch.
+bool gemv_streams_b(uint64_t bytes) { return bytes > (4ull << 20); }
+
 // Split-k shape of a decode GEMV: about four workgroups per CU, each slice a
 // multiple of 32 rows (four waves x eight rows in flight); one slice when
 // the column groups alone fill the device.
@@ -695,11 +714,16 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
         mhip_status st = workspace(ctx, row_blocks * slices * ROWS * n * sizeof(float), &partial);
         if (st != MHIP_OK) return st;
     }
-    hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT>),
-                       dim3(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices),
-                            static_cast<unsigned>(row_blocks)),
-                       dim3(kGemvThreads), 0, ctx->stream, a, b, partial, c, k, n, k_per_slice,
-                       static_cast<uint32_t>(slices), addend, mode);
+    const dim3 grid(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices),
+                    static_cast<unsigned>(row_blocks));
+    if (gemv_streams_b(k * n * sizeof(BT)))
+        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, true>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices), addend, mode);
+    else
+        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, false>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices), addend, mode);
     mhip_status st = mhip::check_launch("matmul (decode partial sums)");
     if (st != MHIP_OK || slices == 1) return st;
     hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>,
@@ -712,11 +736,15 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
 template <int ROWS, class BT>
 mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
                             const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups,
-                            uint32_t row_blocks = 1) {
+                            bool stream, uint32_t row_blocks = 1) {
     uint32_t blocks = 0;
     for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
-    hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT>), dim3(blocks, row_blocks),
-                       dim3(kGemvThreads), 0, ctx->stream, a, k, set);
+    if (stream)
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true>), dim3(blocks, row_blocks),
+                           dim3(kGemvThreads), 0, ctx->stream, a, k, set);
+    else
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false>), dim3(blocks, row_blocks),
+                           dim3(kGemvThreads), 0, ctx->stream, a, k, set);
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
     hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups, row_blocks),
@@ -823,17 +851,17 @@ namespace {
 template <class BT>
 mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                               const GemvSet& set, int epilogue, const RopeEpi& rq,
-                              const RopeEpi& rk, uint32_t g) {
+                              const RopeEpi& rk, uint32_t g, bool stream) {
     switch (rows) {
-        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g);
-        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g);
+        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
         default:
-            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g,
+            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream,
                                           static_cast<uint32_t>(rows / kGemvMaxRows));
     }
 }
@@ -859,6 +887,7 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     if (epilogue == kGemvRopeQK && (count < 2 || !rope)) return MHIP_LAYOUT_UNSUPPORTED;
     GemvSet set{};
     set.count = count;
+    bool stream = false;
     uint64_t floats = 0, blocks = 0, groups = 0;
     uint64_t offsets[3];
     for (int i = 0; i < count; ++i) {
@@ -880,6 +909,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
         g.k_per_slice = k_per_slice;
         g.col_groups = static_cast<uint32_t>((t.n + kGemvCols - 1) / kGemvCols);
         g.slices = static_cast<uint32_t>(slices);
+        // The set streams its matrices when any of them is large.
+        if (gemv_streams_b(k * t.n * (bf16_weights ? 2 : 4))) stream = true;
         g.first_block = static_cast<uint32_t>(blocks);
         g.first_group = static_cast<uint32_t>(groups);
         offsets[i] = floats;
@@ -919,8 +950,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     float* partial = static_cast<float*>(scratch);
     for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
     const uint32_t g = static_cast<uint32_t>(groups);
-    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g)
-                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g);
+    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream)
+                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream);
 }
 
 }  // namespace mhip

@@ -310,3 +310,25 @@ def test_kv_write_through_the_executor(ex):
     assert not ex.write_zeroed_kv_store("kv_tq", (4, 2), KV_TQ4, 2)
     with pytest.raises(KernelError):
         ex.read_tensor("kv_tq")
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8, 16, 40])
+def test_gated_matmul_is_bit_identical_to_its_parts(ex, orc, rows):
+    """gated-matmul equals matmul, matmul and silu-mul dispatched separately,
+    bit for bit (src/tests_conformance.rs:486-565): decode rows take the fused
+    GEMV set, 40 rows the separate kernels; also into an offered output
+    buffer of the right size."""
+    hidden, ffn = 256, 344
+    ex.write_tensor("g.x", orc.hashed_values(rows * hidden, 11 + rows).reshape(rows, hidden))
+    ex.write_tensor("g.w", orc.hashed_values(hidden * ffn, 12).reshape(hidden, ffn))
+    ex.write_tensor("g.u", orc.hashed_values(hidden * ffn, 13).reshape(hidden, ffn))
+    ex.execute(inv("matmul", ["g.x", "g.w"], "g.gate"))
+    ex.execute(inv("matmul", ["g.x", "g.u"], "g.up"))
+    ex.execute(inv("silu-mul", ["g.gate", "g.up"], "g.want"))
+    want = ex.read_tensor("g.want")
+    ex.execute(inv("gated-matmul", ["g.x", "g.w", "g.u"], "g.out"))
+    assert_bitexact(ex.read_tensor("g.out"), want)
+    ex.execute(inv("gated-matmul", ["g.x", "g.w", "g.u"], "g.out"))  # offered buffer
+    assert_bitexact(ex.read_tensor("g.out"), want)
+    for name in ("g.x", "g.w", "g.u", "g.gate", "g.up", "g.want", "g.out"):
+        ex.release_tensor(name)
