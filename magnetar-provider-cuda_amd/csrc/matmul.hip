@@ -149,24 +149,21 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
     *tn = in_group / rows_in_group;
 }
 
-// blockIdx.y is the k split: the workgroup sums k in [y * k_split,
-// min(K, (y + 1) * k_split)) and, with more than one split, writes that
-// partial product to C + y * M * N (no addend) for splitk_reduce_kernel.
+// One tile's product, C[m0 .., n0 ..] summed over k in [k_begin, k_end),
+// written to out[(row - out_r0) * ldo + (col - out_c0)] for the rows < M and
+// columns < N, plus the addend when addend_mode is 1 or 2. LDS (`lds`) is
+// free on entry and again on return.
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
-__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_kernel(
-    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
-    uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
+__device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT* __restrict__ B,
+                                          uint64_t M, uint64_t K, uint64_t N, uint64_t m0,
+                                          uint64_t n0, uint64_t k_begin, uint64_t k_end,
+                                          float* lds, float* __restrict__ out, uint64_t out_r0,
+                                          uint64_t out_c0, uint64_t ldo,
+                                          const float* __restrict__ addend, int addend_mode) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     constexpr int T = Cfg::kThreads;
-    extern __shared__ float lds[];
     // Buffer b of the A slices at lds + b * kLdsA; the B slices follow both.
     float* const lds_b0 = lds + 2 * Cfg::kLdsA;
-
-    uint32_t tm, tn;
-    tile_coords(static_cast<uint32_t>((M + BM - 1) / BM), static_cast<uint32_t>((N + BN - 1) / BN),
-                &tm, &tn);
-    const uint64_t m0 = static_cast<uint64_t>(tm) * BM;
-    const uint64_t n0 = static_cast<uint64_t>(tn) * BN;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -181,10 +178,7 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const uint64_t k_begin = static_cast<uint64_t>(blockIdx.y) * k_split;
-    const uint64_t k_end = min(K, k_begin + k_split);  // slices past k_end are zero-filled
-    if (gridDim.y > 1) C += static_cast<uint64_t>(blockIdx.y) * M * N;
-
+    // Slices past k_end are zero-filled.
     float4 ra[Cfg::kAChunks], rb[Cfg::kBChunks];
     auto load = [&](uint64_t k0) {
         if constexpr (A_T)
@@ -239,14 +233,116 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
                 const uint64_t row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * lk + (r % 4);
                 if (row < M) {
                     float v = acc[i][j][r];
-                    if (gridDim.y == 1) {
-                        if (addend_mode == 1) v = v + addend[col];
-                        else if (addend_mode == 2) v = v + addend[row * N + col];
-                    }
-                    C[row * N + col] = v;
+                    if (addend_mode == 1) v = v + addend[col];
+                    else if (addend_mode == 2) v = v + addend[row * N + col];
+                    out[(row - out_r0) * ldo + (col - out_c0)] = v;
                 }
             }
         }
+    }
+}
+
+// One tile per workgroup. blockIdx.y is the k split: the workgroup sums k in
+// [y * k_split, min(K, (y + 1) * k_split)) and, with more than one split,
+// writes that partial product to C + y * M * N (no addend) for
+// splitk_reduce_kernel.
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_kernel(
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
+    uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
+    extern __shared__ float lds[];
+    uint32_t tm, tn;
+    tile_coords(static_cast<uint32_t>((M + BM - 1) / BM), static_cast<uint32_t>((N + BN - 1) / BN),
+                &tm, &tn);
+    const uint64_t k_begin = static_cast<uint64_t>(blockIdx.y) * k_split;
+    const uint64_t k_end = min(K, k_begin + k_split);
+    const bool split = gridDim.y > 1;
+    float* out = split ? C + static_cast<uint64_t>(blockIdx.y) * M * N : C;
+    gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT>(
+        A, B, M, K, N, static_cast<uint64_t>(tm) * BM, static_cast<uint64_t>(tn) * BN, k_begin,
+        k_end, lds, out, 0, 0, N, addend, split ? 0 : addend_mode);
+}
+
+// Stream-K: the (tile, k slice) units, tile-major (tile t = tm * tiles_n +
+// tn, its slices in k order), are dealt in equal runs of `per` to the
+// workgroups, so every CU does the same MFMA work however the tiles divide.
+// Workgroup w covers units [w * per, (w + 1) * per); per <= slices per tile,
+// so that run touches at most two tiles, and the part of the j-th one goes to
+// slot 2w + j as a BM x BN tile for stream_reduce_kernel.
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_stream_kernel(
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ slots, uint64_t M,
+    uint64_t K, uint64_t N, uint64_t per) {
+    extern __shared__ float lds[];
+    const uint64_t tiles_n = (N + BN - 1) / BN;
+    const uint64_t kslices = (K + BK - 1) / BK;
+    const uint64_t total = (M + BM - 1) / BM * tiles_n * kslices;
+    uint64_t u = static_cast<uint64_t>(blockIdx.x) * per;
+    const uint64_t end = min(total, u + per);
+    for (int seg = 0; seg < 2 && u < end; ++seg) {
+        const uint64_t t = u / kslices, s0 = u % kslices;
+        const uint64_t s1 = min(kslices, s0 + (end - u));
+        const uint64_t m0 = t / tiles_n * BM, n0 = t % tiles_n * BN;
+        float* slot = slots + (2 * static_cast<uint64_t>(blockIdx.x) + seg) * (BM * BN);
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT>(A, B, M, K, N, m0, n0, s0 * BK,
+                                                         min(K, s1 * BK), lds, slot, m0, n0, BN,
+                                                         nullptr, 0);
+        u += s1 - s0;
+    }
+}
+
+// C = the stream-K slots covering each output's tile, added in k order (the
+// workgroups' order), + addend: deterministic. Four consecutive outputs per
+// thread; `vec` (N % 4 == 0, aligned C and addend): one dwordx4 each.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void stream_reduce_kernel(const float* __restrict__ slots,
+                                                            float* __restrict__ C, uint64_t M,
+                                                            uint64_t N, uint64_t kslices,
+                                                            uint64_t per,
+                                                            const float* __restrict__ addend,
+                                                            int addend_mode, int vec) {
+    const uint64_t total = M * N;
+    const uint64_t i = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= total) return;
+    const uint64_t tiles_n = (N + BN - 1) / BN;
+    auto slot_of = [&](uint64_t row, uint64_t col, uint64_t* w_first, uint64_t* w_last) {
+        const uint64_t t = row / BM * tiles_n + col / BN;
+        *w_first = t * kslices / per;
+        *w_last = ((t + 1) * kslices - 1) / per;
+        return t * kslices;  // the tile's first unit
+    };
+    auto at = [&](uint64_t w, uint64_t first_unit, uint64_t row, uint64_t col) {
+        const uint64_t seg = w * per < first_unit ? 1 : 0;
+        return slots + (2 * w + seg) * (BM * BN) + (row % BM) * BN + col % BN;
+    };
+    if (vec && i + 3 < total) {
+        const uint64_t row = i / N, col = i % N;  // four columns of one tile (BN % 4 == 0)
+        uint64_t w0, w1;
+        const uint64_t first = slot_of(row, col, &w0, &w1);
+        float4 v = mhip::load_nt(reinterpret_cast<const float4*>(at(w0, first, row, col)));
+        for (uint64_t w = w0 + 1; w <= w1; ++w) {
+            const float4 p = mhip::load_nt(reinterpret_cast<const float4*>(at(w, first, row, col)));
+            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        }
+        if (addend_mode == 1) {
+            const float4 b = *reinterpret_cast<const float4*>(addend + col);
+            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        } else if (addend_mode == 2) {
+            const float4 b = *reinterpret_cast<const float4*>(addend + i);
+            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        }
+        *reinterpret_cast<float4*>(C + i) = v;
+        return;
+    }
+    for (uint64_t e = i; e < i + 4 && e < total; ++e) {
+        const uint64_t row = e / N, col = e % N;
+        uint64_t w0, w1;
+        const uint64_t first = slot_of(row, col, &w0, &w1);
+        float v = *at(w0, first, row, col);
+        for (uint64_t w = w0 + 1; w <= w1; ++w) v += *at(w, first, row, col);
+        if (addend_mode == 1) v = v + addend[col];
+        else if (addend_mode == 2) v = v + addend[e];
+        C[e] = v;
     }
 }
 
@@ -306,23 +402,56 @@ uint64_t choose_splits(uint64_t tiles, uint64_t k, uint64_t slots, uint64_t bk,
     return (k + per - 1) / per;
 }
 
+// How one tile configuration covers an m x k x n product on `slots`
+// resident workgroups: k splits of whole tiles (split-k, one launch per
+// round of tiles), or stream-K runs of `per` (tile, k slice) units when that
+// gives every workgroup less work (tiles that do not divide the device).
+struct GemmPlan {
+    uint64_t tiles, kslices;
+    uint64_t splits, k_split;  // split-k
+    bool stream;
+    uint64_t per, groups;      // stream-K: units per workgroup, workgroups
+    uint64_t steps;            // k slices per workgroup along the critical path
+    double partial_tiles;      // partial-result traffic, in whole products (m x n)
+};
+
+GemmPlan plan_gemm(uint64_t m, uint64_t k, uint64_t n, uint64_t bm, uint64_t bn, uint64_t bk,
+                   uint64_t slots) {
+    GemmPlan p{};
+    p.tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    p.kslices = (k + bk - 1) / bk;
+    p.splits = choose_splits(p.tiles, k, slots, bk, &p.k_split);
+    const uint64_t rounds = (p.tiles * p.splits + slots - 1) / slots;
+    p.steps = rounds * ((p.k_split + bk - 1) / bk);
+    p.partial_tiles = p.splits > 1 ? static_cast<double>(p.splits) : 0.0;
+    const uint64_t units = p.tiles * p.kslices;
+    const uint64_t per = (units + slots - 1) / slots;
+    // Stream-K when it cuts the critical path by over 10 %; its runs must
+    // stay within two tiles (per <= kslices) and, as splits do, cover at
+    // least 256 of k (8 slices of 32), or partial results outweigh them.
+    if (p.tiles < slots && per <= p.kslices && per * bk >= 256 && per * 10 < p.steps * 9) {
+        p.stream = true;
+        p.per = per;
+        p.groups = (units + per - 1) / per;
+        p.steps = per;
+        p.partial_tiles = static_cast<double>(p.groups + p.tiles) / static_cast<double>(p.tiles);
+    }
+    return p;
+}
+
 // Estimated seconds for an m x k x n product with one tile configuration:
-// rounds of resident workgroups times each one's share of the MFMA work (at
-// the configuration's measured fraction of peak, shared by the workgroups a
-// CU holds), plus the split-k reduce's traffic. Picks between the 128 x 128
-// and 256 x 256 kernels.
+// the critical path's k slices at the configuration's measured fraction of
+// peak (shared by the workgroups a CU holds), plus the partial results'
+// traffic. Picks between the 128 x 128 and 256 x 256 kernels.
 double gemm_seconds(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n, uint64_t bm,
                     uint64_t bn, uint64_t bk, uint64_t lds_bytes, double efficiency) {
     const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
     const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / lds_bytes);
-    const uint64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
-    uint64_t k_split = k;
-    const uint64_t splits = choose_splits(tiles, k, per_cu * cus, bk, &k_split);
-    const uint64_t rounds = (tiles * splits + per_cu * cus - 1) / (per_cu * cus);
+    const GemmPlan p = plan_gemm(m, k, n, bm, bn, bk, per_cu * cus);
     const double cu_flops = 157.3e12 / 256.0;  // dense fp32 MFMA per CU per second
     const double slot_flops = cu_flops * efficiency / static_cast<double>(per_cu);
-    double t = static_cast<double>(rounds) * 2.0 * bm * bn * k_split / slot_flops;
-    if (splits > 1) t += static_cast<double>(splits + 1) * m * n * 4.0 / 5.0e12;
+    double t = static_cast<double>(p.steps) * 2.0 * bm * bn * bk / slot_flops;
+    if (p.partial_tiles > 0.0) t += (p.partial_tiles + 1.0) * m * n * 4.0 / 5.0e12;
     return t;
 }
 
@@ -335,41 +464,59 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     // Resident workgroups per CU: as many tiles as fit the 160 KB of LDS.
     const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
     const uint64_t slots = per_cu * (ctx->compute_units ? ctx->compute_units : 256);
-    uint64_t k_split = k;
-    const uint64_t splits = choose_splits(tiles, k, slots, BK, &k_split);
-    float* target = c;
-    if (splits > 1) {
-        mhip_status st = workspace(ctx, splits * m * n * sizeof(float), &target);
-        if (st != MHIP_OK) return st;
-    }
+    const GemmPlan plan = plan_gemm(m, k, n, BM, BN, BK, slots);
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
     if (!configured) {
-        (void)hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        (void)hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        for (const void* f : {reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
+                              reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>)})
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
+    const uint64_t groups_out = (m * n + 1023) / 1024;
+    if (groups_out >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: output too large");
+    // dwordx4 reduction: whole rows of 4 and 16-byte aligned output and addend.
+    const int vec4 = n % 4 == 0 && mhip::aligned16(c) && (mode == 0 || mhip::aligned16(addend));
+
+    if (plan.stream) {
+        float* slot_mem = nullptr;
+        mhip_status st = workspace(ctx, plan.groups * 2 * BM * BN * sizeof(float), &slot_mem);
+        if (st != MHIP_OK) return st;
+        const dim3 grid(static_cast<unsigned>(plan.groups));
+        if (vec)
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>), grid,
+                               dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
+        else
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>), grid,
+                               dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
+        st = mhip::check_launch("matmul (MFMA stream-K)");
+        if (st != MHIP_OK) return st;
+        hipLaunchKernelGGL((stream_reduce_kernel<BM, BN>), dim3(static_cast<unsigned>(groups_out)),
+                           dim3(256), 0, ctx->stream, slot_mem, c, m, n, plan.kslices, plan.per,
+                           addend, mode, vec4);
+        return mhip::check_launch("matmul (stream-K reduction)");
+    }
+
+    float* target = c;
+    if (plan.splits > 1) {
+        mhip_status st = workspace(ctx, plan.splits * m * n * sizeof(float), &target);
+        if (st != MHIP_OK) return st;
+    }
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(plan.splits));
     if (vec)
         hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
-                           mode, k_split);
+                           mode, plan.k_split);
     else
         hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
-                           mode, k_split);
+                           mode, plan.k_split);
     mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
-    if (st != MHIP_OK || splits == 1) return st;
-    const uint64_t groups = (m * n + 1023) / 1024;
-    if (groups >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: output too large");
-    // dwordx4 path: whole rows of 4 and 16-byte aligned output and addend.
-    const int vec4 = n % 4 == 0 && mhip::aligned16(c) && (mode == 0 || mhip::aligned16(addend));
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(groups)), dim3(256), 0,
-                       ctx->stream, target, c, m, n, static_cast<uint32_t>(splits), addend, mode,
+    if (st != MHIP_OK || plan.splits == 1) return st;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(groups_out)), dim3(256), 0,
+                       ctx->stream, target, c, m, n, static_cast<uint32_t>(plan.splits), addend, mode,
                        vec4);
     return mhip::check_launch("matmul (split-k reduction)");
 }

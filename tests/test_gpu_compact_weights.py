@@ -34,6 +34,7 @@ def same_bits(a, b):
     (9, 300, 130, False, False, 0),      # MFMA, ragged edges
     (64, 2048, 256, False, False, 0),    # MFMA with split-k
     (512, 512, 512, False, False, 2),
+    (400, 2050, 1900, False, False, 2),  # MFMA stream-K
     (40, 96, 72, False, True, 1),        # b stored [n, k]
     (33, 64, 47, True, True, 0),
     (1, 64, 10, False, False, 0),        # n % 4 != 0: tile path

@@ -187,3 +187,51 @@ def test_row_blocked_gemv(dev, orc, m, k, n, mode):
         block = ops.matmul(dev, dev.upload(np.ascontiguousarray(a[r:r + 8])), db, addend=part,
                            addend_mode=mode).numpy()
         assert_bitexact(got[r:r + 8], block)
+
+
+@pytest.mark.parametrize("m,k,n,mode", [(400, 2050, 1900, 0), (400, 2050, 1900, 1), (130, 4096, 4000, 2),
+                                        (40, 4096, 4096, 1)])
+def test_stream_k_products(dev, orc, m, k, n, mode):
+    """Products whose tiles do not divide the device run stream-K (equal runs
+    of (tile, k slice) units per workgroup, partial tiles summed in k order):
+    ragged edges, a short last run, both tile sizes, against the oracle, and
+    the fused addend bit-identical to matmul + add."""
+    from magnetar_hip import ops
+    a = orc.uniform(m * k, 51 + m, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 52 + n, -1.0, 1.0).reshape(k, n)
+    addend = None
+    if mode == 1:
+        addend = orc.uniform(n, 53, -1.0, 1.0)
+    elif mode == 2:
+        addend = orc.uniform(m * n, 54, -1.0, 1.0).reshape(m, n)
+    da, db = dev.upload(a), dev.upload(b)
+    dadd = dev.upload(addend) if addend is not None else None
+    got = ops.matmul(dev, da, db, addend=dadd, addend_mode=mode).numpy()
+    want, st = orc.matmul(a, b, addend=addend, addend_mode=mode)
+    assert st == 0
+    err = max_normwise_err(got, want)
+    print(f"stream-K {m}x{k}x{n} mode {mode}: normwise err {err:.2e}")
+    assert err <= TOL
+    again = ops.matmul(dev, da, db, addend=dadd, addend_mode=mode).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))  # deterministic
+    if mode:
+        plain = ops.matmul(dev, da, db)
+        summed = (ops.add(dev, plain, dadd) if mode == 2 else ops.bias_add(dev, plain, dadd)).numpy()
+        assert np.array_equal(got.view(np.uint32), summed.view(np.uint32))
+
+
+def test_stream_k_prefill_projection(dev, orc):
+    """The gate/up projection of a 512-token Llama-2-7B prefill (512 x 4096
+    x 11008, 86 tiles of 256 x 256): 16 sampled rows against the oracle and a
+    checksum of the whole product, C x = A (B x), in f64."""
+    from magnetar_hip import ops
+    m, k, n = 512, 4096, 11008
+    a = orc.uniform(m * k, 61, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 62, -1.0, 1.0).reshape(k, n)
+    c = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
+    for r in np.linspace(0, m - 1, 16).astype(int):
+        assert max_normwise_err(c[r:r + 1], orc.matmul_rows(a, b, int(r), int(r) + 1)) <= TOL
+    x = np.random.default_rng(1).standard_normal(n)
+    lhs = c.astype(np.float64) @ x
+    rhs = a.astype(np.float64) @ (b.astype(np.float64) @ x)
+    assert np.max(np.abs(lhs - rhs)) / np.max(np.abs(rhs)) <= TOL
