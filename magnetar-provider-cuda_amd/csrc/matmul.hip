@@ -528,95 +528,138 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
 constexpr int kGemvThreads = 256;
 constexpr int kGemvCols = 256;  // columns per workgroup: 64 lanes x 4
 
-// One workgroup's share of a decode GEMV: column group `cg` (256 columns)
-// and k slice `slice`. Its 4 waves split the slice's rows and meet in LDS.
+// How a GEMV lane reads CPL consecutive columns of one row of B: f32 as one
+// dwordx4, compact bf16 as 8 bytes (CPL 4) or one dwordx4 of 8 values (CPL
+// 8), kept raw in registers until widened (exactly) at use.
+template <class BT, int CPL>
+struct GemvLoad;
+template <>
+struct GemvLoad<float, 4> {
+    using Raw = float4;
+    template <bool NT>
+    static __device__ __forceinline__ Raw load(const float* p) {
+        if constexpr (NT) return load4_nt(p);
+        else return load4(p);
+    }
+    static __device__ __forceinline__ float4 part(const Raw& v, int) { return v; }
+};
+template <>
+struct GemvLoad<uint16_t, 4> {
+    using Raw = uint2;
+    template <bool NT>
+    static __device__ __forceinline__ Raw load(const uint16_t* p) {
+        if constexpr (NT) {
+            const mhip::u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const mhip::u32x2*>(p));
+            return make_uint2(t.x, t.y);
+        } else {
+            return *reinterpret_cast<const uint2*>(p);
+        }
+    }
+    static __device__ __forceinline__ float4 part(const Raw& v, int) { return mhip::widen(v); }
+};
+template <>
+struct GemvLoad<uint16_t, 8> {
+    using Raw = uint4;
+    template <bool NT>
+    static __device__ __forceinline__ Raw load(const uint16_t* p) {
+        if constexpr (NT) return mhip::load_nt(reinterpret_cast<const uint4*>(p));
+        else return *reinterpret_cast<const uint4*>(p);
+    }
+    static __device__ __forceinline__ float4 part(const Raw& v, int h) {
+        return mhip::widen(h ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y));
+    }
+};
+
+// One workgroup's share of a decode GEMV: column group `cg` (64 * CPL
+// columns, CPL per lane) and k slice `slice`. Its 4 waves split the slice's
+// rows and meet in LDS. Each column's sum runs over the same k in the same
+// order whatever CPL is, so CPL changes loads, not results.
 // `direct`: write C (+ addend) itself (the only slice); otherwise write the
 // slice's partial sums for the reduction. STREAM: read B non-temporally (a
 // matrix larger than an XCD's L2, read once per call); a small B is read
 // through the caches, where it stays between calls. (A template parameter:
 // a run-time choice inside the load loop doubled the registers.)
-template <int ROWS, class BT, bool STREAM>
+template <int ROWS, class BT, bool STREAM, int CPL>
 __device__ __forceinline__ void gemv_partial_body(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t cg,
     uint32_t slice, bool direct, const float* __restrict__ addend, int addend_mode) {
-    __shared__ float4 red[4][ROWS][64];
+    constexpr int H = CPL / 4;  // float4 groups per lane
+    using L = GemvLoad<BT, CPL>;
+    __shared__ float4 red[4][ROWS][H][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t col = static_cast<uint64_t>(cg) * kGemvCols + lane * 4;
-    const bool live = col < N;
+    const uint64_t col = static_cast<uint64_t>(cg) * (64 * CPL) + lane * CPL;
+    const bool live = col < N;  // N % CPL == 0: a live lane's columns are all in range
     const uint64_t k_begin = static_cast<uint64_t>(slice) * k_per_slice;
     const uint64_t k_end = min(K, k_begin + k_per_slice);
-    float4 acc[ROWS];
+    float4 acc[ROWS][H];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) {
-        // Rows of B in flight per lane: 8 dwordx4 of f32, 16 8-byte bf16 loads
-        // (the same bytes in flight either way).
-        constexpr int kU = sizeof(BT) == 4 ? 8 : 16;
-        uint64_t kk = k_begin + wave;
-        for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
-            float4 bv[kU];
+    for (int r = 0; r < ROWS; ++r)
 #pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                if constexpr (STREAM) bv[u] = load4_nt(B + (kk + 4 * u) * N + col);
-                else bv[u] = load4(B + (kk + 4 * u) * N + col);
-            }
+        for (int h = 0; h < H; ++h) acc[r][h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto fma_row = [&](const typename L::Raw& raw, uint64_t k) {
 #pragma unroll
-            for (int u = 0; u < kU; ++u) {
-#pragma unroll
-                for (int r = 0; r < ROWS; ++r) {
-                    const float a = A[r * K + kk + 4 * u];
-                    acc[r].x = __builtin_fmaf(a, bv[u].x, acc[r].x);
-                    acc[r].y = __builtin_fmaf(a, bv[u].y, acc[r].y);
-                    acc[r].z = __builtin_fmaf(a, bv[u].z, acc[r].z);
-                    acc[r].w = __builtin_fmaf(a, bv[u].w, acc[r].w);
-                }
-            }
-        }
-        for (; kk < k_end; kk += 4) {
-            float4 bv;
-            if constexpr (STREAM) bv = load4_nt(B + kk * N + col);
-            else bv = load4(B + kk * N + col);
+        for (int h = 0; h < H; ++h) {
+            const float4 b = L::part(raw, h);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                const float a = A[r * K + kk];
-                acc[r].x = __builtin_fmaf(a, bv.x, acc[r].x);
-                acc[r].y = __builtin_fmaf(a, bv.y, acc[r].y);
-                acc[r].z = __builtin_fmaf(a, bv.z, acc[r].z);
-                acc[r].w = __builtin_fmaf(a, bv.w, acc[r].w);
+                const float a = A[r * K + k];
+                acc[r][h].x = __builtin_fmaf(a, b.x, acc[r][h].x);
+                acc[r][h].y = __builtin_fmaf(a, b.y, acc[r][h].y);
+                acc[r][h].z = __builtin_fmaf(a, b.z, acc[r][h].z);
+                acc[r][h].w = __builtin_fmaf(a, b.w, acc[r][h].w);
             }
         }
+    };
+    if (live) {
+        // 128 bytes of B rows in flight per lane.
+        constexpr int kU = 128 / sizeof(typename L::Raw);
+        uint64_t kk = k_begin + wave;
+        for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
+            typename L::Raw bv[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) bv[u] = L::template load<STREAM>(B + (kk + 4 * u) * N + col);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) fma_row(bv[u], kk + 4 * u);
+        }
+        for (; kk < k_end; kk += 4) fma_row(L::template load<STREAM>(B + kk * N + col), kk);
     }
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) red[wave][r][lane] = acc[r];
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int h = 0; h < H; ++h) red[wave][r][h][lane] = acc[r][h];
     __syncthreads();
     if (wave != 0 || !live) return;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        float4 v = red[0][r][lane];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            const float4 o = red[w][r][lane];
-            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
-        }
-        if (direct) {
-            if (addend_mode == 1) {
-                const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
-                v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
-            } else if (addend_mode == 2) {
-                const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + col);
-                v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+        for (int h = 0; h < H; ++h) {
+            const uint64_t c = col + 4 * h;
+            float4 v = red[0][r][h][lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) {
+                const float4 o = red[w][r][h][lane];
+                v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
             }
-            *reinterpret_cast<float4*>(C + r * N + col) = v;
-        } else {
-            *reinterpret_cast<float4*>(partial + (static_cast<uint64_t>(slice) * ROWS + r) * N + col) = v;
+            if (direct) {
+                if (addend_mode == 1) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(addend + c);
+                    v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+                } else if (addend_mode == 2) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + c);
+                    v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+                }
+                *reinterpret_cast<float4*>(C + r * N + c) = v;
+            } else {
+                *reinterpret_cast<float4*>(partial + (static_cast<uint64_t>(slice) * ROWS + r) * N + c) = v;
+            }
         }
     }
 }
 
 // blockIdx.z is a block of ROWS rows of A and C: each is an independent
 // ROWS-row GEMV with its own partial sums (B is shared through L2).
-template <int ROWS, class BT, bool STREAM>
+template <int ROWS, class BT, bool STREAM, int CPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t slices,
@@ -626,8 +669,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     C += rb * ROWS * N;
     if (partial) partial += rb * slices * ROWS * N;
     if (addend_mode == 2) addend += rb * ROWS * N;
-    gemv_partial_body<ROWS, BT, STREAM>(A, B, partial, C, K, N, k_per_slice, blockIdx.x,
-                                        blockIdx.y, slices == 1, addend, addend_mode);
+    gemv_partial_body<ROWS, BT, STREAM, CPL>(A, B, partial, C, K, N, k_per_slice, blockIdx.x,
+                                             blockIdx.y, slices == 1, addend, addend_mode);
 }
 
 // Sum of the slices' partial sums of 256 columns: wave w adds a fixed
@@ -751,7 +794,7 @@ __device__ __forceinline__ GemvSeg pick(const GemvSet& set, int i) {
     return set.seg[2];
 }
 
-template <int ROWS, class BT, bool STREAM>
+template <int ROWS, class BT, bool STREAM, int CPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const float* __restrict__ A,
                                                                         uint64_t K, GemvSet set) {
     const uint32_t b = blockIdx.x;
@@ -760,7 +803,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const fl
     const GemvSeg s = pick(set, i);
     const uint32_t local = b - s.first_block;
     const uint64_t rb = blockIdx.y;  // row block of ROWS rows
-    gemv_partial_body<ROWS, BT, STREAM>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
+    gemv_partial_body<ROWS, BT, STREAM, CPL>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
                                         s.partial + rb * s.slices * ROWS * s.n, nullptr, K, s.n,
                                         s.k_per_slice, local % s.col_groups, local / s.col_groups,
                                         false, nullptr, 0);
@@ -850,10 +893,29 @@ void gemv_slicing(const mhip_ctx* ctx, uint64_t k, uint64_t n, uint64_t* slices_
     *k_per_slice_out = k_per_slice;
 }
 
+// Compact weights on up to 4 rows read 8 columns per lane (16-byte loads)
+// when every row of B starts 16-byte aligned; otherwise 4.
+template <int ROWS, class BT>
+constexpr bool kGemvWideable = sizeof(BT) == 2 && ROWS <= 4;
+
+template <int ROWS, class BT, int CPL>
+void launch_gemv_partial(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, const BT* b,
+                         float* partial, float* c, uint64_t k, uint64_t n, uint64_t k_per_slice,
+                         uint64_t slices, const float* addend, int mode) {
+    if (stream)
+        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, true, CPL>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices), addend, mode);
+    else
+        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, false, CPL>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices), addend, mode);
+}
+
 template <int ROWS, class BT>
 mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t k,
                         uint64_t n, const float* addend, int mode, uint64_t row_blocks = 1) {
-    const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
+    const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;  // of the reduction
     uint64_t slices, k_per_slice;
     gemv_slicing(ctx, k, n, &slices, &k_per_slice);
     float* partial = nullptr;
@@ -861,16 +923,23 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
         mhip_status st = workspace(ctx, row_blocks * slices * ROWS * n * sizeof(float), &partial);
         if (st != MHIP_OK) return st;
     }
-    const dim3 grid(static_cast<unsigned>(col_groups), static_cast<unsigned>(slices),
+    const bool stream = gemv_streams_b(k * n * sizeof(BT));
+    bool wide = false;
+    if constexpr (kGemvWideable<ROWS, BT>) wide = n % 8 == 0 && mhip::aligned16(b);
+    const uint64_t part_groups = wide ? (n + 511) / 512 : col_groups;
+    const dim3 grid(static_cast<unsigned>(part_groups), static_cast<unsigned>(slices),
                     static_cast<unsigned>(row_blocks));
-    if (gemv_streams_b(k * n * sizeof(BT)))
-        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, true>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices), addend, mode);
-    else
-        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, false>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices), addend, mode);
+    if constexpr (kGemvWideable<ROWS, BT>) {
+        if (wide)
+            launch_gemv_partial<ROWS, BT, 8>(ctx, grid, stream, a, b, partial, c, k, n, k_per_slice,
+                                             slices, addend, mode);
+        else
+            launch_gemv_partial<ROWS, BT, 4>(ctx, grid, stream, a, b, partial, c, k, n, k_per_slice,
+                                             slices, addend, mode);
+    } else {
+        launch_gemv_partial<ROWS, BT, 4>(ctx, grid, stream, a, b, partial, c, k, n, k_per_slice,
+                                         slices, addend, mode);
+    }
     mhip_status st = mhip::check_launch("matmul (decode partial sums)");
     if (st != MHIP_OK || slices == 1) return st;
     hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>,
@@ -880,18 +949,32 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     return mhip::check_launch("matmul (decode reduction)");
 }
 
+template <int ROWS, class BT, int CPL>
+void launch_gemv_set_partial(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, uint64_t k,
+                             const GemvSet& set) {
+    if (stream)
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true, CPL>), grid, dim3(kGemvThreads),
+                           0, ctx->stream, a, k, set);
+    else
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false, CPL>), grid, dim3(kGemvThreads),
+                           0, ctx->stream, a, k, set);
+}
+
+// `wide`: the set's segments were planned with 8 columns per lane.
 template <int ROWS, class BT>
 mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
                             const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups,
-                            bool stream, uint32_t row_blocks = 1) {
+                            bool stream, bool wide, uint32_t row_blocks = 1) {
     uint32_t blocks = 0;
     for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
-    if (stream)
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true>), dim3(blocks, row_blocks),
-                           dim3(kGemvThreads), 0, ctx->stream, a, k, set);
-    else
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false>), dim3(blocks, row_blocks),
-                           dim3(kGemvThreads), 0, ctx->stream, a, k, set);
+    const dim3 grid(blocks, row_blocks);
+    if constexpr (kGemvWideable<ROWS, BT>) {
+        if (wide) launch_gemv_set_partial<ROWS, BT, 8>(ctx, grid, stream, a, k, set);
+        else launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set);
+    } else {
+        if (wide) return MHIP_LAYOUT_UNSUPPORTED;
+        launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set);
+    }
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
     hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups, row_blocks),
@@ -998,17 +1081,17 @@ namespace {
 template <class BT>
 mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                               const GemvSet& set, int epilogue, const RopeEpi& rq,
-                              const RopeEpi& rk, uint32_t g, bool stream) {
+                              const RopeEpi& rk, uint32_t g, bool stream, bool wide) {
     switch (rows) {
-        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
-        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream);
+        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
         default:
-            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream,
+            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide,
                                           static_cast<uint32_t>(rows / kGemvMaxRows));
     }
 }
@@ -1035,6 +1118,11 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     GemvSet set{};
     set.count = count;
     bool stream = false;
+    // Compact weights on up to 4 rows: 8 columns per lane when every matrix
+    // allows 16-byte loads (as launch_gemv decides for one).
+    bool wide = bf16_weights && rows <= 4;
+    for (int i = 0; i < count; ++i)
+        if (targets[i].n % 8 != 0 || !aligned16(targets[i].b)) wide = false;
     uint64_t floats = 0, blocks = 0, groups = 0;
     uint64_t offsets[3];
     for (int i = 0; i < count; ++i) {
@@ -1054,7 +1142,7 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
                             : nullptr;
         g.n = t.n;
         g.k_per_slice = k_per_slice;
-        g.col_groups = static_cast<uint32_t>((t.n + kGemvCols - 1) / kGemvCols);
+        g.col_groups = static_cast<uint32_t>((t.n + (wide ? 511 : 255)) / (wide ? 512 : 256));
         g.slices = static_cast<uint32_t>(slices);
         // The set streams its matrices when any of them is large.
         if (gemv_streams_b(k * t.n * (bf16_weights ? 2 : 4))) stream = true;
@@ -1063,7 +1151,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
         offsets[i] = floats;
         floats += (slices * rows * t.n + 63) / 64 * 64;
         blocks += g.col_groups * slices;
-        if (!(epilogue == kGemvSiluMul && i == 1)) groups += g.col_groups;
+        // The reduction always takes 256 columns per workgroup.
+        if (!(epilogue == kGemvSiluMul && i == 1)) groups += (t.n + kGemvCols - 1) / kGemvCols;
     }
     if (blocks >= (1ULL << 31)) return MHIP_LAYOUT_UNSUPPORTED;
     RopeEpi rq{}, rk{};
@@ -1097,8 +1186,8 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     float* partial = static_cast<float*>(scratch);
     for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
     const uint32_t g = static_cast<uint32_t>(groups);
-    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream)
-                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream);
+    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream, wide)
+                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream, wide);
 }
 
 }  // namespace mhip

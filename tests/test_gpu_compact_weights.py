@@ -30,6 +30,8 @@ def same_bits(a, b):
     (1, 4096, 4096, False, False, 0),    # decode GEMV
     (3, 1000, 516, False, False, 2),     # GEMV, ragged k, residual
     (8, 256, 64, False, False, 1),       # GEMV, bias
+    (4, 2048, 2056, False, False, 1),    # GEMV, 8 columns per lane, bias
+    (2, 512, 1032, False, False, 2),     # GEMV, 8 columns per lane, one split, residual
     (32, 256, 688, False, False, 2),     # row-blocked GEMV, residual
     (9, 300, 130, False, False, 0),      # MFMA, ragged edges
     (64, 2048, 256, False, False, 0),    # MFMA with split-k
