@@ -190,7 +190,7 @@ def test_row_blocked_gemv(dev, orc, m, k, n, mode):
 
 
 @pytest.mark.parametrize("m,k,n,mode", [(400, 2050, 1900, 0), (400, 2050, 1900, 1), (130, 4096, 4000, 2),
-                                        (40, 4096, 4096, 1)])
+                                        (40, 4096, 4096, 1), (400, 2050, 1901, 2)])
 def test_stream_k_products(dev, orc, m, k, n, mode):
     """Products whose tiles do not divide the device run stream-K (equal runs
     of (tile, k slice) units per workgroup, partial tiles summed in k order):

@@ -121,6 +121,40 @@ def test_silu_special_values(dev, orc):
     assert np.array_equal(np.signbit(got[finite]), np.signbit(want[finite]))
 
 
+def test_elementwise_at_baseline_size(dev, orc):
+    """[8192, 4096] (the BASELINE shape): add, mul, bias and residual add
+    bit-exact, silu and silu-mul within the tolerance, against the oracle."""
+    from magnetar_hip import ops
+    shape = (8192, 4096)
+    n = shape[0] * shape[1]
+    a = orc.normal(n, 71, 0.0, 1.0).reshape(shape)
+    b = orc.normal(n, 72, 0.0, 1.0).reshape(shape)
+    bias = orc.normal(shape[1], 73, 0.0, 1.0)
+    da, db = dev.upload(a), dev.upload(b)
+    assert_bitexact(ops.add(dev, da, db).numpy(), orc.add(a, b)[0], "add")
+    assert_bitexact(ops.mul(dev, da, db).numpy(), orc.mul(a, b)[0], "mul")
+    assert_bitexact(ops.bias_add(dev, da, dev.upload(bias)).numpy(), orc.bias_add(a, bias)[0], "bias")
+    assert max_rel_err(ops.silu(dev, da).numpy(), orc.silu(a)[0], 1e-37) <= SILU_TOL
+    assert max_rel_err(ops.silu_mul(dev, da, db).numpy(), orc.silu_mul(a, b)[0], 1e-37) <= SILU_TOL
+
+
+def test_embedding_table_past_2_gib(dev, orc):
+    """The C3 lookup: 8192 ids into a [128000, 4096] table (2.1 GB, so row
+    offsets pass 2^31 bytes), bit-exact. Entry (r, c) holds the bit pattern
+    r * 4096 + c (distinct, finite, denormal for r < 2048)."""
+    from magnetar_hip import ops
+    vocab, dim = 128000, 4096
+    table = (np.arange(vocab, dtype=np.uint32)[:, None] * dim
+             + np.arange(dim, dtype=np.uint32)[None, :]).view(np.float32)
+    ids = orc.token_ids(8192, 74, vocab)
+    ids[:3] = [vocab - 1, 0, 2048]
+    got = ops.embedding(dev, dev.upload(table), dev.upload(ids)).numpy()
+    assert dev.check_flags() == 0
+    want, st = orc.embedding(table, ids)
+    assert st == 0
+    assert_bitexact(got, want)
+
+
 # ---- half precision ---------------------------------------------------------
 
 HALF = {"f16": 0, "bf16": 1}
