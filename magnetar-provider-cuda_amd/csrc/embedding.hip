@@ -49,6 +49,23 @@ __global__ __launch_bounds__(kThreads) void embedding_vec_kernel(
     }
 }
 
+// Rows of whole 1024-float blocks: one workgroup per block, one dwordx4 per
+// thread (short-lived workgroups keep reads and writes interleaved).
+template <class T>
+__global__ __launch_bounds__(kThreads) void embedding_block_kernel(
+    const T* __restrict__ table, uint64_t vocab, uint64_t dim4, const float* __restrict__ ids,
+    uint64_t num_ids, float* __restrict__ out, uint32_t* flags) {
+    const uint64_t blocks_per_row = dim4 / kThreads;
+    const uint64_t row = blockIdx.x / blocks_per_row;
+    const uint64_t c = (blockIdx.x % blocks_per_row) * kThreads + threadIdx.x;
+    uint64_t id = 0;
+    if (!valid_embedding_id(ids[row], vocab, &id)) {
+        if (c == 0) atomicOr(flags, MHIP_FLAG_EMBEDDING_INVALID_ID);
+        return;
+    }
+    mhip::store_nt(reinterpret_cast<float4*>(out) + row * dim4 + c, mhip::load4_nt(table + (id * dim4 + c) * 4));
+}
+
 // Any dim or alignment: one wave per row, scalar copies.
 template <class T>
 __global__ __launch_bounds__(kThreads) void embedding_scalar_kernel(
@@ -77,7 +94,11 @@ mhip_status embedding_impl(mhip_ctx* ctx, const T* table, uint64_t vocab, uint64
     const bool vec = dim % 4 == 0 && (reinterpret_cast<uintptr_t>(table) & table_align) == 0 &&
                      mhip::aligned16(out);
     const uint64_t dim4 = dim / 4;
-    if (vec && dim4 > 256) {
+    if (vec && dim4 >= 256 && dim4 % 256 == 0 && num_ids * (dim4 / 256) < (1ull << 31)) {
+        hipLaunchKernelGGL((embedding_block_kernel<T>),
+                           dim3(static_cast<unsigned>(num_ids * (dim4 / 256))), dim3(kThreads), 0,
+                           ctx->stream, table, vocab, dim4, ids, num_ids, out, ctx->flags);
+    } else if (vec && dim4 > 256) {
         hipLaunchKernelGGL((embedding_vec_kernel<256, 4, T>), dim3(static_cast<unsigned>(num_ids)),
                            dim3(kThreads), 0, ctx->stream, table, vocab, dim4, ids, num_ids, out,
                            ctx->flags);

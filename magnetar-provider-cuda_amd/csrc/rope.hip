@@ -127,28 +127,45 @@ using mhip::rope_rotate;
 // Interleaved pairing, vector path: cols, head_width and dimension are
 // multiples of 4, so a dwordx4 at head offset j holds pairs j/2 and j/2+1
 // (both rotated or both passed through).
+// The row's first kVecBatch vectors per thread are loaded before the sin/cos
+// table is built, so the table's math overlaps the loads; longer rows
+// continue in a loop.
+constexpr int kVecBatch = 4;
+
 __global__ __launch_bounds__(kThreads) void rope_interleaved_vec_kernel(RopeArgs a) {
     extern __shared__ float lds[];
     float* cs = lds;
     float* sn = lds + a.half;
     const uint64_t row = blockIdx.x;
-    row_sincos(a, row, cs, sn);
-    __syncthreads();
     const uint64_t cols4 = a.cols / 4, hw4 = a.head_width / 4;
     const float4* x4 = reinterpret_cast<const float4*>(a.in) + row * cols4;
     float4* o4 = reinterpret_cast<float4*>(a.out) + row * cols4;
-    for (uint64_t c = threadIdx.x; c < cols4; c += kThreads) {
+    float4 v[kVecBatch];
+#pragma unroll
+    for (int u = 0; u < kVecBatch; ++u) {
+        const uint64_t c = threadIdx.x + static_cast<uint64_t>(u) * kThreads;
+        if (c < cols4) v[u] = mhip::load_nt(x4 + c);
+    }
+    row_sincos(a, row, cs, sn);
+    __syncthreads();
+    auto rotate_store = [&](uint64_t c, float4 x) {
         const uint64_t j = (c % hw4) * 4;
-        float4 v = mhip::load_nt(x4 + c);
         if (j < a.dimension) {
             const uint64_t p = j / 2;
             float4 r;
-            rope_rotate(v.x, v.y, cs[p], sn[p], &r.x, &r.y);
-            rope_rotate(v.z, v.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
-            v = r;
+            rope_rotate(x.x, x.y, cs[p], sn[p], &r.x, &r.y);
+            rope_rotate(x.z, x.w, cs[p + 1], sn[p + 1], &r.z, &r.w);
+            x = r;
         }
-        mhip::store_nt(o4 + c, v);
+        mhip::store_nt(o4 + c, x);
+    };
+#pragma unroll
+    for (int u = 0; u < kVecBatch; ++u) {
+        const uint64_t c = threadIdx.x + static_cast<uint64_t>(u) * kThreads;
+        if (c < cols4) rotate_store(c, v[u]);
     }
+    for (uint64_t c = threadIdx.x + static_cast<uint64_t>(kVecBatch) * kThreads; c < cols4; c += kThreads)
+        rotate_store(c, mhip::load_nt(x4 + c));
 }
 
 // Half-split pairing, vector path: half is a multiple of 4, so the dwordx4
