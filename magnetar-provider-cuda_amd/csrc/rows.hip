@@ -73,21 +73,25 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
         live = false;  // still takes part in the group reduction below
     }
     const TT* xr = in + src * cols;
-    float4 x[VPT];
+    const float4* w4 = weight ? reinterpret_cast<const float4*>(weight + row * weight_row_stride)
+                              : nullptr;
+    float4 x[VPT], wv[VPT];
     float ss = 0.0f;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
         x[v] = (live && c < cols4) ? mhip::load4_nt(xr + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
+        // The gain goes out with the row, not after the reduction.
+        if (w4 && live && c < cols4) wv[v] = w4[c];
     }
+#pragma unroll
+    for (int v = 0; v < VPT; ++v)
+        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
     ss = group_reduce<G>(ss, SumOp{}, scratch);
     if (!live) return;
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
     float4* c4 = copy ? reinterpret_cast<float4*>(copy) + row * cols4 : nullptr;
-    const float4* w4 = weight ? reinterpret_cast<const float4*>(weight + row * weight_row_stride)
-                              : nullptr;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
@@ -95,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
             if (c4) mhip::store_nt(c4 + c, x[v]);
             float4 y;
             if (w4) {
-                float4 w = w4[c];
+                const float4 w = wv[v];
                 y = make_float4(x[v].x * inv * w.x, x[v].y * inv * w.y, x[v].z * inv * w.z,
                                 x[v].w * inv * w.w);
             } else {
