@@ -146,12 +146,25 @@ __device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D
     return s;
 }
 
+// Short prefills, whose query tiles alone would leave most of the device
+// idle, split the key range: chunk c of nchunks covers key tiles [c *
+// chunk_tiles, (c + 1) * chunk_tiles) counted from key 0, and writes, per
+// query, the chunk's normalised output, running max (log2 domain) and weight
+// sum for attn_prefill_combine_kernel. The split depends on one sequence's
+// shape only, so a batch still equals its separate calls.
+struct PrefillSplit {
+    uint32_t nchunks;      // 1: no split, the kernel writes the output itself
+    uint32_t chunk_tiles;
+    float* part_o;         // [batch * seq][heads][nchunks][VD]
+    float* part_ml;        // [batch * seq][heads][nchunks][2]
+};
+
 // The workgroup walks its key tiles double-buffered in LDS, each tile loaded
 // straight from global memory into LDS (no register staging), which keeps
 // the kernel within 256 registers: two waves per SIMD, one from each of the
 // two workgroups a CU holds, overlap each other's MFMA and softmax phases.
 template <int D, int VD>
-__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, PrefillSplit sp) {
     apply_advance(a);
     using Cfg = PrefillCfg<D, VD>;
     extern __shared__ float lds[];
@@ -166,8 +179,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
     // it heaviest first (ids of one head's query tiles, dealt to XCDs by
     // query tile, left XCDs with 2.4x the work of others).
     const uint64_t qtiles = (a.seq + Cfg::kBQ - 1) / Cfg::kBQ;
-    const uint64_t pairs = gridDim.x / qtiles;
-    const uint64_t bid = blockIdx.x;
+    const uint64_t chunk = blockIdx.x % sp.nchunks;
+    const uint64_t pairs = gridDim.x / sp.nchunks / qtiles;
+    const uint64_t bid = blockIdx.x / sp.nchunks;
     const uint64_t qt = qtiles - 1 - bid / pairs;
     const uint64_t bh = bid % pairs;
     const uint64_t head = bh % a.heads, b = bh / a.heads;
@@ -240,23 +254,34 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) vx[j] = (((l32 >> 2) ^ (4 * half + j)) << 2) + (l32 & 3);
 
-    // Tile i sits in buffer i & 1 (K and V); tile i+1 is loaded straight into
-    // the other buffer while tile i is used (that buffer held tile i-1, whose
-    // readers all passed the previous barrier).
-    if (ntiles > 0) {
-        load_k(tile_begin, kbuf(0));
-        load_v(tile_begin, vbuf(0));
+    // This workgroup's tiles [i_begin, i_end) of the ntiles from tile_begin:
+    // all of them, or the part inside its key chunk.
+    int i_begin = 0, i_end = ntiles;
+    if (sp.nchunks > 1) {
+        const int64_t first = static_cast<int64_t>(tile_begin / Cfg::kBKV);
+        const int64_t c0 = static_cast<int64_t>(chunk) * sp.chunk_tiles - first;
+        i_begin = static_cast<int>(min<int64_t>(max<int64_t>(c0, 0), ntiles));
+        i_end = static_cast<int>(min<int64_t>(max<int64_t>(c0 + sp.chunk_tiles, 0), ntiles));
+    }
+
+    // The j-th tile walked sits in buffer j & 1 (K and V); the next one is
+    // loaded straight into the other buffer while it is used (that buffer
+    // held the previous tile, whose readers all passed the previous barrier).
+    if (i_end > i_begin) {
+        load_k(tile_begin + static_cast<uint64_t>(i_begin) * Cfg::kBKV, kbuf(0));
+        load_v(tile_begin + static_cast<uint64_t>(i_begin) * Cfg::kBKV, vbuf(0));
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int i = 0; i < ntiles; ++i) {
+    for (int i = i_begin; i < i_end; ++i) {
+        const int j = i - i_begin;
         const uint64_t k0 = tile_begin + static_cast<uint64_t>(i) * Cfg::kBKV;
-        if (i + 1 < ntiles) {
-            load_k(k0 + Cfg::kBKV, kbuf(i + 1));
-            load_v(k0 + Cfg::kBKV, vbuf(i + 1));
+        if (i + 1 < i_end) {
+            load_k(k0 + Cfg::kBKV, kbuf(j + 1));
+            load_v(k0 + Cfg::kBKV, vbuf(j + 1));
         }
         if (wave_in(k0)) {
-            v16f s_cur = tile_scores<D>(kbuf(i), qf, l32, half);
+            v16f s_cur = tile_scores<D>(kbuf(j), qf, l32, half);
             // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q; bit
             // j of `admit` says whether tile key j is admitted.
             const int lo_r = min(max(rel_lo - i * Cfg::kBKV, 0), Cfg::kBKV);
@@ -289,7 +314,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
             const float keep = (psum == 0.0f && alpha == 1.0f) || l_new == 0.0f ? 1.0f : (l * alpha) * inv;
 #pragma unroll
             for (int r = 0; r < 16; ++r) s_cur[r] *= inv;
-            const float* sv = vbuf(i);
+            const float* sv = vbuf(j);
 #pragma unroll
             for (int vb = 0; vb < VD / 32; ++vb) {
 #pragma unroll
@@ -310,7 +335,17 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
     }
 
     // Register r of block vb holds O[q][vb*32 + 8*(r/4) + 4*half + r%4].
-    if (q_live) {
+    if (q_live && sp.nchunks > 1) {
+        const uint64_t rec = ((b * a.seq + q) * a.heads + head) * sp.nchunks + chunk;
+        float* po = sp.part_o + rec * VD;
+#pragma unroll
+        for (int vb = 0; vb < VD / 32; ++vb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(po + vb * 32 + 8 * g + 4 * half) =
+                    make_float4(o[vb][4 * g], o[vb][4 * g + 1], o[vb][4 * g + 2], o[vb][4 * g + 3]);
+        if (half == 0) *reinterpret_cast<float2*>(sp.part_ml + 2 * rec) = make_float2(m, l);
+    } else if (q_live) {
         float* orow = O + q * o_ld;
 #pragma unroll
         for (int vb = 0; vb < VD / 32; ++vb)
@@ -321,11 +356,86 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a) {
     }
 }
 
+// Chunk records of split attention live in the context's workspace.
+mhip_status attention_workspace(mhip_ctx* ctx, size_t bytes, float** out) {
+    void* p = nullptr;
+    mhip_status st = mhip::workspace(ctx, bytes, &p);
+    *out = static_cast<float*>(p);
+    return st;
+}
+
+// Merges a split prefill's chunk records per (query row, head): out = sum_c
+// w_c o_c with w_c = l_c 2^(m_c - M) / sum_c' l_c' 2^(m_c' - M), in chunk
+// order; no admitted key in any chunk gives zeros. VD / 4 threads per (row,
+// head), one float4 of the output each.
+template <int VD>
+__global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnArgs a, uint64_t rows,
+                                                                   PrefillSplit sp) {
+    constexpr int kLanes = VD / 4;
+    constexpr int kItems = 256 / kLanes;
+    const uint64_t item = static_cast<uint64_t>(blockIdx.x) * kItems + threadIdx.x / kLanes;
+    const int t = threadIdx.x % kLanes;
+    if (item >= rows * a.heads) return;
+    const uint64_t row = item / a.heads, head = item % a.heads;
+    const uint64_t b = row / a.seq, q = row % a.seq;
+    const float* ml = sp.part_ml + 2 * item * sp.nchunks;
+    const float* po = sp.part_o + item * sp.nchunks * VD + 4 * t;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < sp.nchunks; ++c) M = fmaxf(M, ml[2 * c]);
+    float total = 0.0f;
+    if (M != -INFINITY)
+        for (uint32_t c = 0; c < sp.nchunks; ++c)
+            if (ml[2 * c + 1] > 0.0f) total += ml[2 * c + 1] * exp2f(ml[2 * c] - M);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (total > 0.0f) {
+        const float inv_total = 1.0f / total;
+        for (uint32_t c = 0; c < sp.nchunks; ++c) {
+            const float l = ml[2 * c + 1];
+            if (!(l > 0.0f)) continue;
+            const float w = l * exp2f(ml[2 * c] - M) * inv_total;
+            const float4 o = *reinterpret_cast<const float4*>(po + c * VD);
+            acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
+        }
+    }
+    *reinterpret_cast<float4*>(a.out + b * a.o_bs + q * (a.heads * VD) + head * VD + 4 * t) = acc;
+}
+
+// Key chunks for a prefill whose query tiles (per sequence) fill under the
+// device's resident slots (two workgroups per CU): enough chunks of at
+// least 4 key tiles to fill them, at most 16.
+void prefill_split(const mhip_ctx* ctx, const AttnArgs& a, uint64_t qtiles, uint64_t kbkv,
+                   uint32_t* nchunks, uint32_t* chunk_tiles) {
+    *nchunks = 1;
+    *chunk_tiles = 0;
+    const uint64_t slots = 2 * static_cast<uint64_t>(ctx->compute_units ? ctx->compute_units : 256);
+    const uint64_t per_sequence = a.heads * qtiles;
+    const uint64_t kv_tiles = (a.kv_seq + kbkv - 1) / kbkv;
+    if (per_sequence >= slots || kv_tiles < 8) return;
+    uint64_t n = std::min<uint64_t>((slots + per_sequence - 1) / per_sequence, kv_tiles / 4);
+    n = std::min<uint64_t>(n, 16);
+    if (n < 2) return;
+    const uint64_t per = (kv_tiles + n - 1) / n;
+    *chunk_tiles = static_cast<uint32_t>(per);
+    *nchunks = static_cast<uint32_t>((kv_tiles + per - 1) / per);
+}
+
 template <int D, int VD>
 mhip_status launch_prefill(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
     using Cfg = PrefillCfg<D, VD>;
-    const uint64_t blocks = batch * a.heads * ((a.seq + Cfg::kBQ - 1) / Cfg::kBQ);
+    const uint64_t qtiles = (a.seq + Cfg::kBQ - 1) / Cfg::kBQ;
+    PrefillSplit sp{};
+    prefill_split(ctx, a, qtiles, Cfg::kBKV, &sp.nchunks, &sp.chunk_tiles);
+    const uint64_t blocks = batch * a.heads * qtiles * sp.nchunks;
     if (blocks >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention: too many query tiles");
+    const uint64_t rows = batch * a.seq;
+    if (sp.nchunks > 1) {
+        const uint64_t records = rows * a.heads * sp.nchunks;
+        float* part = nullptr;
+        mhip_status st = attention_workspace(ctx, records * (VD + 2) * sizeof(float), &part);
+        if (st != MHIP_OK) return st;
+        sp.part_o = part;
+        sp.part_ml = part + records * VD;
+    }
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;
     if (!configured) {
@@ -334,8 +444,14 @@ mhip_status launch_prefill(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
         configured = true;
     }
     hipLaunchKernelGGL((attn_prefill_kernel<D, VD>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), lds, ctx->stream, a);
-    return mhip::check_launch("attention (MFMA prefill)");
+                       dim3(256), lds, ctx->stream, a, sp);
+    mhip_status st = mhip::check_launch("attention (MFMA prefill)");
+    if (st != MHIP_OK || sp.nchunks == 1) return st;
+    const uint64_t items = rows * a.heads;
+    constexpr uint64_t kItems = 256 / (VD / 4);
+    hipLaunchKernelGGL((attn_prefill_combine_kernel<VD>), dim3(static_cast<unsigned>((items + kItems - 1) / kItems)),
+                       dim3(256), 0, ctx->stream, a, rows, sp);
+    return mhip::check_launch("attention (prefill chunk merge)");
 }
 
 // ---------------------------------------------------------------------------
@@ -569,13 +685,6 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
         v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w;
     }
     *reinterpret_cast<float4*>(a.out + b * a.o_bs + head * D + 4 * t) = v;
-}
-
-mhip_status attention_workspace(mhip_ctx* ctx, size_t bytes, float** out) {
-    void* p = nullptr;
-    mhip_status st = mhip::workspace(ctx, bytes, &p);
-    *out = static_cast<float*>(p);
-    return st;
 }
 
 template <int D4, int GT>

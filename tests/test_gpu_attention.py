@@ -97,6 +97,7 @@ def test_reference_sweep(dev, orc, case):
     (70, 70, 2, 2, 4, True),     # tiled prefill
     (200, 200, 2, 2, 64, True),  # MFMA prefill
     (130, 130, 1, 1, 128, False),
+    (300, 300, 2, 2, 128, True),  # MFMA prefill split over key chunks
 ])
 def test_large_finite_values_stay_finite(dev, shape):
     seq, kv, h, hkv, d, causal = shape
@@ -175,6 +176,25 @@ def test_batch_equals_separate_calls(dev, orc, seq, kv):
         one = run(dev, q[b * seq:(b + 1) * seq], k[b * kv:(b + 1) * kv], v[b * kv:(b + 1) * kv],
                   seq_len=seq, kv_rows=kv, head_count=h, head_dimension=d, causal=True)
         assert_bitexact(batched[b * seq:(b + 1) * seq], one, f"batch {b}")
+
+
+def test_c5_prefill_attention_split_over_key_chunks(dev, orc):
+    """S512 H32 d128 causal (the C5 prefill): 128 query tiles leave the device
+    idle, so the key range is split into chunks merged afterwards. Three heads
+    against the oracle, and query 0 sees only key 0 (its output is V row 0)."""
+    from magnetar_hip import ops
+    S, H, d = 512, 32, 128
+    q = orc.normal(S * H * d, 81).reshape(S, H * d)
+    k = orc.normal(S * H * d, 82).reshape(S, H * d)
+    v = orc.normal(S * H * d, 83).reshape(S, H * d)
+    got = ops.attention(dev, dev.upload(q), dev.upload(k), dev.upload(v),
+                        ops.attention_params(S, S, H, d, causal=True)).numpy()
+    for h0 in (0, 17, 31):
+        want = oracle(orc, q, k, v, heads=(h0, h0 + 1), seq_len=S, kv_rows=S, head_count=H,
+                      head_dimension=d, causal=True)
+        cols = slice(h0 * d, (h0 + 1) * d)
+        assert max_normwise_err(got[:, cols], want[:, cols]) <= TOL
+    assert np.max(np.abs(got[0] - v[0])) <= 1e-6 * np.max(np.abs(v[0]))
 
 
 def test_c4_prefill_shape(dev, orc):
