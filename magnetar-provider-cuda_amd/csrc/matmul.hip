@@ -109,6 +109,22 @@ __device__ __forceinline__ void load_slice(float4 (&regs)[CHUNKS], const T* __re
     }
 }
 
+// The same slice when it lies wholly inside the matrix (rows r0 .. r0 + ROWS
+// and columns c0 .. c0 + COLS in range, 16-byte aligned rows): plain
+// dwordx4 loads with no bounds checks, issued back to back.
+template <int ROWS, int COLS, int CHUNKS, int THREADS, class T>
+__device__ __forceinline__ void load_slice_interior(float4 (&regs)[CHUNKS], const T* __restrict__ g,
+                                                    uint64_t ld, uint64_t r0, uint64_t c0) {
+    constexpr int kChunksPerRow = COLS / 4;
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        const int chunk = threadIdx.x + i * THREADS;
+        const int r = chunk / kChunksPerRow;
+        const int c = (chunk % kChunksPerRow) * 4;
+        regs[i] = load4(g + (r0 + r) * ld + c0 + c);
+    }
+}
+
 // Stores the chunks into an LDS slice laid out [k][mn] with row stride S.
 // TRANSPOSED: the global rows were mn and the columns k (write 4 words down
 // a column); otherwise the global rows were k (write one dwordx4).
@@ -178,9 +194,23 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Slices past k_end are zero-filled.
+    // Slices past k_end are zero-filled. A slice wholly inside the matrices
+    // (every slice of an interior tile but the last partial one) takes the
+    // unchecked loads.
     float4 ra[Cfg::kAChunks], rb[Cfg::kBChunks];
+    const bool interior_tile = VEC && m0 + BM <= M && n0 + BN <= N;
     auto load = [&](uint64_t k0) {
+        if (interior_tile && k0 + BK <= k_end) {
+            if constexpr (A_T)
+                load_slice_interior<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T>(ra, A, M, k0, m0);
+            else
+                load_slice_interior<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T>(ra, A, K, m0, k0);
+            if constexpr (B_T)
+                load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, K, n0, k0);
+            else
+                load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, N, k0, n0);
+            return;
+        }
         if constexpr (A_T)
             load_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, VEC>(ra, A, M, k0, m0, k_end, M);
         else
