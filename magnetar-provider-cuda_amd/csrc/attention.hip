@@ -119,7 +119,7 @@ __device__ __forceinline__ void dma_tile(const float* g, uint64_t ld, uint64_t k
         const int row = slot / kChunksPerRow;
         const int chunk = (slot % kChunksPerRow) ^ (row & 7);
         uint64_t key = k0 + row;
-        if (key >= rows) key = rows - 1;
+        if (k0 + 32 > rows && key >= rows) key = rows - 1;  // only the last tile clamps
         const float* src = g + key * ld + chunk * 4;
         __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
     }
@@ -284,17 +284,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
             v16f s_cur = tile_scores<D>(kbuf(j), qf, l32, half);
             // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q; bit
             // j of `admit` says whether tile key j is admitted.
-            const int lo_r = min(max(rel_lo - i * Cfg::kBKV, 0), Cfg::kBKV);
-            const int hi_r = min(max(rel_hi - i * Cfg::kBKV, 0), Cfg::kBKV);
-            const uint64_t span = ((1ull << hi_r) - 1ull) & ~((1ull << lo_r) - 1ull);
-            const uint32_t mine = static_cast<uint32_t>(span) >> (4 * half);
+            // A tile every query of the wave admits whole needs no mask.
+            if (!(k0 >= all_lo && k0 + Cfg::kBKV <= all_hi)) {
+                const int lo_r = min(max(rel_lo - i * Cfg::kBKV, 0), Cfg::kBKV);
+                const int hi_r = min(max(rel_hi - i * Cfg::kBKV, 0), Cfg::kBKV);
+                const uint64_t span = ((1ull << hi_r) - 1ull) & ~((1ull << lo_r) - 1ull);
+                const uint32_t mine = static_cast<uint32_t>(span) >> (4 * half);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = 8 * (r / 4) + (r % 4);
+                    s_cur[r] = (mine >> key) & 1u ? s_cur[r] : -INFINITY;
+                }
+            }
             float tile_max = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = 8 * (r / 4) + (r % 4);
-                s_cur[r] = (mine >> key) & 1u ? s_cur[r] : -INFINITY;
-                tile_max = fmaxf(tile_max, s_cur[r]);
-            }
+            for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s_cur[r]);
             tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
             // Every lane runs the update (the MFMAs below need the whole wave);
             // a query with no admitted key yet keeps m = -inf, l = 0, o = 0.
