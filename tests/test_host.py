@@ -98,3 +98,17 @@ def test_kernel_entry_points_refuse_a_null_context():
     assert lib.mhip_add_f32(None, None, None, None, 16) == 8
     assert lib.mhip_matmul_f32(None, None, None, None, 2, 2, 2, 0, 0, None, 0) == 8
     assert lib.mhip_sync(None) == 8
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 prints why and exits non-zero
+    before touching a device."""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    done = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120)
+    assert done.returncode != 0
+    line = json.loads(done.stdout.strip().splitlines()[-1])
+    assert "one GPU" in line["error"]
