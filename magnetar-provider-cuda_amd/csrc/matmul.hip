@@ -4,29 +4,33 @@
 // src/kernels.cu:1262-1306): optional transposes (A stored [k, m], B stored
 // [n, k]), f32 accumulation, the addend added to the finished sum.
 //
-// Two kernels, chosen by shape:
-//  - m > kGemvMaxRows: fp32 MFMA tiles. A workgroup owns a BM x BN tile of C
-//    and walks k in BK slices. Both operand slices are staged k-major in LDS
-//    (A as [BK][BM], B as [BK][BN]), double-buffered: the next slice is
-//    loaded from global memory into registers while the MFMAs run on the
-//    current one. Each wave owns WM x WN of the tile as (WM/32) x (WN/32)
+// Two kernel families, chosen by shape:
+//  - MFMA tiles. A workgroup owns a BM x BN tile of C and walks k in BK
+//    slices. Both operand slices are staged k-major in LDS (A as [BK][BM], B
+//    as [BK][BN]), double-buffered: the next slice is loaded from global
+//    memory into registers while the MFMAs run on the current one (plain
+//    dwordx4 loads with no bounds checks when the slice lies wholly inside
+//    the matrices). Each wave owns WM x WN of the tile as (WM/32) x (WN/32)
 //    v_mfma_f32_32x32x2_f32 accumulators; per k step of 2, lane l feeds
 //    A[row l%32][k + l/32] and B[k + l/32][col l%32] straight from LDS, so
 //    operand reads are 32 consecutive words per half-wave (no bank
 //    conflicts). LDS rows are padded: +1 word where a slice is stored
 //    transposed (scattered 4-byte writes land in distinct banks), +4 where
-//    it is copied as dwordx4. Tiles are ordered so that consecutive tiles
-//    share a block row of A and each of the 8 XCDs (own L2) gets a contiguous
-//    band of tiles. When there are too few tiles to fill the device (m = 512
-//    gives 128 tiles of 128 x 128 for 256 CUs), k is split over up to 8
-//    workgroups per tile; their partial tiles go to a workspace and a second
-//    launch adds them in split order (deterministic) with the addend.
+//    it is copied as dwordx4. Two configurations: 256 x 256 tiles of 8 waves
+//    (one per CU) for large products, 128 x 128 of 4 waves (two per CU)
+//    otherwise, picked by a time model. Tiles are ordered so that
+//    consecutive tiles share a block row of A and each of the 8 XCDs (own
+//    L2) gets a contiguous band of tiles. When the tiles cannot fill the
+//    device, k is split: over up to 8 workgroups per tile (split-k), or in
+//    equal runs of (tile, k slice) units per workgroup (stream-K) when the
+//    tiles divide the device badly; partial tiles go to a workspace and a
+//    second launch adds them in k order (deterministic) with the addend.
 //  - m <= kGemvMaxRows (decode), or up to 32 rows of a small product in row
-//    blocks of 8: the work is reading B once (HBM-bound), so
-//    each wave streams 256 columns of B with dwordx4 loads over one k slice,
-//    keeping m x 4 partial sums per lane; partial sums per k slice go to a
-//    workspace and a second launch adds them in a fixed order
-//    (deterministic), four waves per 256 columns.
+//    blocks of 8: the work is reading B once (HBM-bound), so each wave
+//    streams 256 columns of B (512 for compact bf16 weights on up to 4 rows)
+//    with 16-byte loads over one k slice, keeping m x 4 partial sums per
+//    lane; partial sums per k slice go to a workspace and a second launch
+//    adds them in a fixed order (deterministic), four waves per 256 columns.
 #include "common.hpp"
 #include "internal.hpp"
 
