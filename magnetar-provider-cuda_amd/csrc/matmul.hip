@@ -1083,11 +1083,17 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
     // wherever the model expects them to finish first, split-k included.
     using Big = TileCfg<256, 256, 32, 64, 128, false, false>;
     using Small = TileCfg<128, 128, 32, 64, 64, false, false>;
-    const bool big = !ta && !tb &&
-                     gemm_seconds(ctx, m, k, n, 256, 256, 32, Big::kLdsFloats * sizeof(float), 0.81) <
-                         gemm_seconds(ctx, m, k, n, 128, 128, 32, Small::kLdsFloats * sizeof(float), 0.70);
-    if (big)
-        return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+    const bool big = gemm_seconds(ctx, m, k, n, 256, 256, 32, Big::kLdsFloats * sizeof(float), 0.81) <
+                     gemm_seconds(ctx, m, k, n, 128, 128, 32, Small::kLdsFloats * sizeof(float), 0.70);
+    if (big) {
+        if (!ta && !tb)
+            return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        if (ta && !tb)
+            return launch_mfma<256, 256, 32, 64, 128, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        if (!ta && tb)
+            return launch_mfma<256, 256, 32, 64, 128, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        return launch_mfma<256, 256, 32, 64, 128, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+    }
     if (!ta && !tb)
         return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     if (ta && !tb)
