@@ -235,3 +235,22 @@ def test_stream_k_prefill_projection(dev, orc):
     lhs = c.astype(np.float64) @ x
     rhs = a.astype(np.float64) @ (b.astype(np.float64) @ x)
     assert np.max(np.abs(lhs - rhs)) / np.max(np.abs(rhs)) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+def test_large_tile_path_with_transposed_operands(dev, orc, ta, tb):
+    """The 256 x 256 tile kernel with A stored [k, m] and/or B stored [n, k]:
+    ragged edges, against the oracle, and bit-identical to the same product
+    with the operands stored untransposed (same tiles, same k order)."""
+    from magnetar_hip import ops
+    m, k, n = 4100, 96, 4164
+    a = orc.uniform(m * k, 91, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 92, -1.0, 1.0).reshape(k, n)
+    a_in = np.ascontiguousarray(a.T) if ta else a
+    b_in = np.ascontiguousarray(b.T) if tb else b
+    got = ops.matmul(dev, dev.upload(a_in), dev.upload(b_in), ta, tb).numpy()
+    want, st = orc.matmul(a, b)
+    assert st == 0
+    assert max_normwise_err(got, want) <= TOL
+    plain = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
