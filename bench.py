@@ -34,6 +34,10 @@ HEADLINE = "matmul_4096"
 TRAFFIC: dict = {"matmul_4096": 470_302_720}  # profiles/matmul_4096_mfma_gemm.md
 
 
+# Untimed GPU time each case runs before its warm-up and timed launches.
+PREHEAT_S = 0.1
+
+
 def seed(config: int, tensor: int) -> int:
     return 0x4D414732 ^ (config << 16) ^ tensor
 
@@ -46,7 +50,19 @@ class Case:
         self.name, self.launch, self.work, self.bound, self.shape = name, launch, work, bound, shape
         self.tokens = tokens
 
-    def measure(self, dev, steps, warmup):
+    def measure(self, dev, steps, warmup, preheat_s=PREHEAT_S):
+        # The MI355X raises its clock over tens of milliseconds of sustained
+        # load (2.06 -> 2.38 GHz measured on the GEMM with s_memtime against
+        # s_memrealtime), so each case first runs its own launches, untimed,
+        # for `preheat_s` of GPU time; then the W warm-up launches, then
+        # exactly `steps` timed ones.
+        spent, i = 0.0, 0
+        while spent < preheat_s:
+            dev.timer_start()
+            for _ in range(4):
+                self.launch(i)
+                i += 1
+            spent += dev.timer_stop() * 1e-3
         for i in range(warmup):
             self.launch(i)
         dev.sync()
@@ -365,6 +381,8 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--only", default="", help="comma-separated kernel names")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--preheat", type=float, default=PREHEAT_S,
+                        help="untimed seconds of GPU time each case runs first (clock ramp)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
@@ -393,7 +411,7 @@ def main(argv=None):
     for case in cases:
         if only and case.name not in only:
             continue
-        results[case.name] = case.measure(dev, args.steps, args.warmup)
+        results[case.name] = case.measure(dev, args.steps, args.warmup, args.preheat)
         r = results[case.name]
         extra = f"  {r['tokens_per_s']:10.1f} tokens/s" if "tokens_per_s" in r else ""
         print(f"# {case.name:14s} {r['ms']*1e3:9.1f} us  {r['achieved']:8.1f} {r['unit']}  "
@@ -414,6 +432,7 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "preheat_s_per_case": args.preheat,
         "ms_per_step": round(head["ms"], 5) if head else None,
         "higher_is_better": True,
         "scaling": "weak",

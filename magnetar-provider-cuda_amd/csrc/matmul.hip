@@ -6,17 +6,21 @@
 //
 // Two kernel families, chosen by shape:
 //  - MFMA tiles. A workgroup owns a BM x BN tile of C and walks k in BK
-//    slices. Both operand slices are staged k-major in LDS (A as [BK][BM], B
-//    as [BK][BN]), double-buffered: the next slice is loaded from global
-//    memory into registers while the MFMAs run on the current one (plain
-//    dwordx4 loads with no bounds checks when the slice lies wholly inside
-//    the matrices). Each wave owns WM x WN of the tile as (WM/32) x (WN/32)
-//    v_mfma_f32_32x32x2_f32 accumulators; per k step of 2, lane l feeds
-//    A[row l%32][k + l/32] and B[k + l/32][col l%32] straight from LDS, so
-//    operand reads are 32 consecutive words per half-wave (no bank
-//    conflicts). LDS rows are padded: +1 word where a slice is stored
-//    transposed (scattered 4-byte writes land in distinct banks), +4 where
-//    it is copied as dwordx4. Two configurations: 256 x 256 tiles of 8 waves
+//    slices, double-buffered in LDS. Each slice keeps its operand's global
+//    orientation, unpadded: rows along k (B stored [k, n], A stored [k, m])
+//    as they are, rows along m or n (A stored [m, k], B stored [n, k]) with
+//    their 16-byte chunks XOR-swizzled. Interior slices of f32 operands go
+//    straight from global memory to LDS (global_load_lds_dwordx4: no
+//    registers, no LDS write instructions) while the MFMAs run on the other
+//    buffer; edge and partial slices, and compact bf16 B, go through
+//    registers (zero-filled, widened) and one 16-byte LDS write per chunk.
+//    Each wave owns WM x WN of the tile as (WM/32) x (WN/32)
+//    v_mfma_f32_32x32x2_f32 accumulators. A slice's k is summed in the order
+//    8g + 4h + e (group g, lane half h, step e), so a swizzled row gives a
+//    half's four k values of a group in one 16-byte read, and a k-major row
+//    is read as 32 consecutive words per half-wave; every fill path and
+//    transpose uses this order and gives the same bits. Two
+//    configurations: 256 x 256 tiles of 8 waves
 //    (one per CU) for large products, 128 x 128 of 4 waves (two per CU)
 //    otherwise, picked by a time model. Tiles are ordered so that
 //    consecutive tiles share a block row of A and each of the 8 XCDs (own
@@ -31,6 +35,8 @@
 //    with 16-byte loads over one k slice, keeping m x 4 partial sums per
 //    lane; partial sums per k slice go to a workspace and a second launch
 //    adds them in a fixed order (deterministic), four waves per 256 columns.
+#include <type_traits>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -63,12 +69,12 @@ struct TileCfg {
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kMI = WM / 32;
     static constexpr int kNI = WN / 32;
-    // A slice in LDS is [BK][sA]; stored transposed (from [m][k] rows) unless A_T.
-    static constexpr int sA = A_T ? BM + 4 : BM + 1;
-    // B slice in LDS is [BK][sB]; stored transposed (from [n][k] rows) if B_T.
-    static constexpr int sB = B_T ? BN + 1 : BN + 4;
-    static constexpr int kLdsA = BK * sA;
-    static constexpr int kLdsB = BK * sB;
+    // LDS slices keep the operand's global orientation, unpadded: A as
+    // [BK][BM] when stored [k, m] (A_T), else [BM][BK]; B as [BK][BN], or
+    // [BN][BK] when stored [n, k] (B_T). Rows along m or n (BK floats each)
+    // have their 16-byte chunks XOR-swizzled; rows along k are plain.
+    static constexpr int kLdsA = BM * BK;
+    static constexpr int kLdsB = BK * BN;
     static constexpr int kLdsFloats = 2 * (kLdsA + kLdsB);
     // Global slices as (rows x cols) with cols contiguous in memory.
     static constexpr int kARows = A_T ? BK : BM, kACols = A_T ? BM : BK;
@@ -77,7 +83,27 @@ struct TileCfg {
     static constexpr int kBChunks = kBRows * kBCols / 4 / kThreads;
     static_assert(kARows * kACols % (4 * kThreads) == 0, "A slice must split evenly");
     static_assert(kBRows * kBCols % (4 * kThreads) == 0, "B slice must split evenly");
+    static_assert(BK == 32, "swizzled rows hold 8 chunks");
 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// XOR pattern of the 16-byte chunks of row r of an m- or n-major slice (8
+// chunks per row). Distinct over any 8 consecutive rows, and (r & 1, pattern)
+// distinct over 16, so 16-byte reads of one chunk position down 16 rows hit
+// distinct banks.
+__device__ __forceinline__ int chunk_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Float offset in an LDS slice of the 16-byte chunk whose global position is
+// (row r, column c) of a slice with COLS columns; SWZ for m- or n-major rows.
+template <int COLS, bool SWZ>
+__device__ __forceinline__ int chunk_offset(int r, int c) {
+    if constexpr (SWZ)
+        return r * COLS + (((c >> 2) ^ chunk_swizzle(r)) << 2);
+    else
+        return r * COLS + c;
+}
 
 using mhip::elem;
 using mhip::load4;
@@ -129,10 +155,9 @@ __device__ __forceinline__ void load_slice_interior(float4 (&regs)[CHUNKS], cons
     }
 }
 
-// Stores the chunks into an LDS slice laid out [k][mn] with row stride S.
-// TRANSPOSED: the global rows were mn and the columns k (write 4 words down
-// a column); otherwise the global rows were k (write one dwordx4).
-template <int ROWS, int COLS, int CHUNKS, int THREADS, int S, bool TRANSPOSED>
+// Stores the chunks into an LDS slice (one 16-byte write each, at the
+// chunk's possibly swizzled position).
+template <int ROWS, int COLS, int CHUNKS, int THREADS, bool SWZ>
 __device__ __forceinline__ void store_slice(const float4 (&regs)[CHUNKS], float* lds) {
     constexpr int kChunksPerRow = COLS / 4;
 #pragma unroll
@@ -140,14 +165,38 @@ __device__ __forceinline__ void store_slice(const float4 (&regs)[CHUNKS], float*
         const int chunk = threadIdx.x + i * THREADS;
         const int r = chunk / kChunksPerRow;
         const int c = (chunk % kChunksPerRow) * 4;
-        if constexpr (TRANSPOSED) {
-            lds[(c + 0) * S + r] = regs[i].x;
-            lds[(c + 1) * S + r] = regs[i].y;
-            lds[(c + 2) * S + r] = regs[i].z;
-            lds[(c + 3) * S + r] = regs[i].w;
-        } else {
-            *reinterpret_cast<float4*>(lds + r * S + c) = regs[i];
-        }
+        *reinterpret_cast<float4*>(lds + chunk_offset<COLS, SWZ>(r, c)) = regs[i];
+    }
+}
+
+// The same slice copied straight from global memory into LDS (interior
+// slices of f32 operands, 16-byte aligned rows): one global_load_lds_dwordx4
+// fills 64 consecutive 16-byte slots, lane i slot i, so each lane fetches
+// the chunk that belongs in its slot. No registers, no LDS write
+// instructions; completion is tracked by vmcnt (wait before the barrier).
+template <int ROWS, int COLS, int WAVES, bool SWZ>
+__device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t ld, uint64_t r0,
+                                          uint64_t c0, float* lds, int wave, int lane) {
+    constexpr unsigned kChunksPerRow = COLS / 4;
+    static_assert(64 % kChunksPerRow == 0, "an instruction covers whole rows");
+    constexpr unsigned kRowsPerInstr = 64 / kChunksPerRow;
+    constexpr unsigned kPerWave = ROWS / kRowsPerInstr / WAVES;
+    static_assert(kPerWave * kRowsPerInstr * WAVES == ROWS, "slice must split over the waves");
+    // Lane l fills row l / kChunksPerRow of the instruction's rows, slot
+    // l % kChunksPerRow. A swizzled row (8 chunks) r takes chunk
+    // slot ^ (r & 7) ^ ((r >> 3) & 1): r & 7 is the lane's row, and bit 3
+    // flips with the instruction's first row (a multiple of 8).
+    const unsigned lr = static_cast<unsigned>(lane) / kChunksPerRow;
+    const unsigned pos = static_cast<unsigned>(lane) % kChunksPerRow;
+    const unsigned off0 = SWZ ? (pos ^ lr) * 4u : pos * 4u;
+    const unsigned off1 = SWZ ? (pos ^ lr ^ 1u) * 4u : pos * 4u;
+    const float* lane_row = g + lr * ld + c0;
+#pragma unroll
+    for (unsigned j = 0; j < kPerWave; ++j) {
+        const unsigned first = (static_cast<unsigned>(wave) * kPerWave + j) * kRowsPerInstr;
+        const unsigned off = (SWZ && ((first >> 3) & 1u)) ? off1 : off0;
+        const float* src = lane_row + (r0 + first) * ld + off;
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(lds + first * COLS), 16, 0, 0);
     }
 }
 
@@ -182,11 +231,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                                           const float* __restrict__ addend, int addend_mode) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     constexpr int T = Cfg::kThreads;
+    // A rows along m (not A_T) and B rows along n (B_T) are swizzled.
+    constexpr bool kASwz = !A_T, kBSwz = B_T;
+    constexpr bool kBDma = std::is_same<BT, float>::value;  // compact B is widened on the way
     // Buffer b of the A slices at lds + b * kLdsA; the B slices follow both.
     float* const lds_b0 = lds + 2 * Cfg::kLdsA;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int wm = wave / Cfg::kWavesN, wn = wave % Cfg::kWavesN;
     const int lrow = lane & 31, lk = lane >> 5;
 
@@ -198,21 +250,35 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Slices past k_end are zero-filled. A slice wholly inside the matrices
-    // (every slice of an interior tile but the last partial one) takes the
-    // unchecked loads.
+    // Filling buffer `buf` with the slice at k0. A slice wholly inside the
+    // matrices (every slice of an interior tile but the last partial one)
+    // goes straight to LDS (f32 operands) or through unchecked loads
+    // (compact B); any other slice through bounds-checked loads that
+    // zero-fill past k_end and the matrix edges. `issue` starts the fill,
+    // `finish` writes whatever went through registers.
     float4 ra[Cfg::kAChunks], rb[Cfg::kBChunks];
     const bool interior_tile = VEC && m0 + BM <= M && n0 + BN <= N;
-    auto load = [&](uint64_t k0) {
-        if (interior_tile && k0 + BK <= k_end) {
+    auto direct = [&](uint64_t k0) { return interior_tile && k0 + BK <= k_end; };
+    auto issue = [&](uint64_t k0, int buf) {
+        float* la = lds + buf * Cfg::kLdsA;
+        float* lb = lds_b0 + buf * Cfg::kLdsB;
+        if (direct(k0)) {
             if constexpr (A_T)
-                load_slice_interior<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T>(ra, A, M, k0, m0);
+                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, M, k0, m0, la, wave, lane);
             else
-                load_slice_interior<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T>(ra, A, K, m0, k0);
-            if constexpr (B_T)
+                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, K, m0, k0, la, wave, lane);
+            if constexpr (kBDma) {
+                if constexpr (B_T)
+                    dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
+                        reinterpret_cast<const float*>(B), K, n0, k0, lb, wave, lane);
+                else
+                    dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
+                        reinterpret_cast<const float*>(B), N, k0, n0, lb, wave, lane);
+            } else if constexpr (B_T) {
                 load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, K, n0, k0);
-            else
+            } else {
                 load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, N, k0, n0);
+            }
             return;
         }
         if constexpr (A_T)
@@ -224,34 +290,73 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         else
             load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, N, k0, n0, k_end, N);
     };
-    auto store = [&](int buf) {
-        store_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, Cfg::sA, !A_T>(ra, lds + buf * Cfg::kLdsA);
-        store_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, Cfg::sB, B_T>(rb, lds_b0 + buf * Cfg::kLdsB);
+    auto finish = [&](uint64_t k0, int buf) {
+        const bool dma = direct(k0);
+        if (!dma)
+            store_slice<Cfg::kARows, Cfg::kACols, Cfg::kAChunks, T, kASwz>(ra, lds + buf * Cfg::kLdsA);
+        if (!dma || !kBDma)
+            store_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, kBSwz>(rb, lds_b0 + buf * Cfg::kLdsB);
+        __builtin_amdgcn_s_waitcnt(0);  // the direct loads have landed in LDS
+    };
+
+    // Operand reads. Every slice sums k in the order k = 8g + 4h + e over
+    // groups g, halves h and steps e (0..3): at step (g, e) lanes of half h
+    // (lane / 32) feed k = 8g + 4h + e. A swizzled row yields that half's 4
+    // values of a group as one 16-byte read; a k-major slice is read one row
+    // per step. Every fill path and operand orientation uses this order, so
+    // they all give the same bits.
+    const int hsw = lk ^ chunk_swizzle(lrow);  // rows wm*WM + i*32 + lrow share lrow & 15
+    auto compute = [&](int buf) {
+        const float* la = lds + buf * Cfg::kLdsA;
+        const float* lb = lds_b0 + buf * Cfg::kLdsB;
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            mhip::f32x4 a4[Cfg::kMI], b4[Cfg::kNI];
+            if constexpr (kASwz) {
+#pragma unroll
+                for (int i = 0; i < Cfg::kMI; ++i)
+                    a4[i] = *reinterpret_cast<const mhip::f32x4*>(la + (wm * WM + i * 32 + lrow) * BK +
+                                                             (((2 * g) ^ hsw) << 2));
+            }
+            if constexpr (kBSwz) {
+#pragma unroll
+                for (int j = 0; j < Cfg::kNI; ++j)
+                    b4[j] = *reinterpret_cast<const mhip::f32x4*>(lb + (wn * WN + j * 32 + lrow) * BK +
+                                                             (((2 * g) ^ hsw) << 2));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = 8 * g + 4 * lk + e;
+                float af[Cfg::kMI], bf[Cfg::kNI];
+#pragma unroll
+                for (int i = 0; i < Cfg::kMI; ++i) {
+                    if constexpr (kASwz) af[i] = a4[i][e];
+                    else af[i] = la[k * BM + wm * WM + i * 32 + lrow];
+                }
+#pragma unroll
+                for (int j = 0; j < Cfg::kNI; ++j) {
+                    if constexpr (kBSwz) bf[j] = b4[j][e];
+                    else bf[j] = lb[k * BN + wn * WN + j * 32 + lrow];
+                }
+#pragma unroll
+                for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::kNI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
     };
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
-    load(k_begin);
-    store(0);
+    issue(k_begin, 0);
+    finish(k_begin, 0);
     __syncthreads();
     for (uint64_t s = 0; s < slices; ++s) {
         const int buf = static_cast<int>(s & 1);
-        if (s + 1 < slices) load(k_begin + (s + 1) * BK);
-        const float* sa = lds + buf * Cfg::kLdsA + lk * Cfg::sA + wm * WM + lrow;
-        const float* sb = lds_b0 + buf * Cfg::kLdsB + lk * Cfg::sB + wn * WN + lrow;
-#pragma unroll
-        for (int k = 0; k < BK; k += 2) {
-            float af[Cfg::kMI], bf[Cfg::kNI];
-#pragma unroll
-            for (int i = 0; i < Cfg::kMI; ++i) af[i] = sa[k * Cfg::sA + i * 32];
-#pragma unroll
-            for (int j = 0; j < Cfg::kNI; ++j) bf[j] = sb[k * Cfg::sB + j * 32];
-#pragma unroll
-            for (int i = 0; i < Cfg::kMI; ++i)
-#pragma unroll
-                for (int j = 0; j < Cfg::kNI; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (s + 1 < slices) store(buf ^ 1);
+        const uint64_t k_next = k_begin + (s + 1) * BK;
+        if (s + 1 < slices) issue(k_next, buf ^ 1);
+        compute(buf);
+        if (s + 1 < slices) finish(k_next, buf ^ 1);
         __syncthreads();
     }
 

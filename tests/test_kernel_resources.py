@@ -4,8 +4,9 @@ A kernel that spills registers or copies a by-value argument to private
 memory (scratch) runs several times slower and no parity test notices. This
 reads the kernel descriptors of the library's own device code objects (the
 `.hip_fatbin` section of each object under `_build/`, unbundled with the ROCm
-LLVM tools) and requires, per kernel, a zero private segment and no VGPR or
-SGPR spills.
+LLVM tools) and requires, per kernel, a zero private segment and no VGPR
+spills. SGPR spills are allowed while the private segment stays zero: they
+then live in spare VGPR lanes (register moves, not memory).
 """
 import os
 import re
@@ -61,8 +62,7 @@ def test_no_kernel_uses_scratch():
         for obj in objects:
             for name, fields in _kernel_resources(obj, tmp).items():
                 count += 1
-                if any(fields.get(f, 0) for f in ("private_segment_fixed_size", "vgpr_spill_count",
-                                                   "sgpr_spill_count")):
+                if any(fields.get(f, 0) for f in ("private_segment_fixed_size", "vgpr_spill_count")):
                     offenders.append(f"{os.path.basename(obj)}: {name} {fields}")
         assert count > 20, f"only {count} kernels found"
         assert not offenders, "kernels using scratch:\n" + "\n".join(offenders)
