@@ -89,6 +89,7 @@ __device__ __forceinline__ void key_range(const AttnArgs& a, uint64_t qpos, uint
 
 template <int D, int VD>
 struct PrefillCfg {
+    static_assert(D >= 64 && VD >= 64, "rows of at least 16 chunks (the swizzle spans 16)");
     static constexpr int kBQ = 128;            // queries per workgroup (4 waves x 32)
     static constexpr int kBKV = 32;            // keys per tile
     static constexpr int kKTile = kBKV * D;    // floats; rows unpadded, 16-byte chunks swizzled
@@ -102,8 +103,10 @@ typedef __attribute__((address_space(1))) void global_void_t;
 // Rows [k0, k0 + 32) of a row-major [*, W] operand (leading dimension ld)
 // into an LDS tile of 32 x W floats, by direct global -> LDS loads: one
 // instruction fills 1 KB of consecutive 16-byte slots, lane i slot i. Slot
-// (row, c) holds the row's chunk c ^ (row & 7) (XOR swizzle instead of
-// padding, so reads down a column and across a row hit distinct banks). Rows
+// (row, c) holds the row's chunk c ^ (row & 15) (XOR swizzle instead of
+// padding: 16-byte reads of one chunk position down 16 rows, which the LDS
+// serves 16 lanes at a time over its 64 banks, and 4-byte reads across a
+// row hit distinct banks). Rows
 // at or past `rows` repeat row rows - 1 (finite data the caller masks out).
 // Completion is tracked by vmcnt: wait for it before the tile's barrier.
 template <int W>
@@ -111,13 +114,13 @@ __device__ __forceinline__ void dma_tile(const float* g, uint64_t ld, uint64_t k
                                          float* tile, int wave, int lane) {
     constexpr int kChunksPerRow = W / 4;
     constexpr int kInstrPerWave = 32 * W / 4 / 64 / 4;
-    static_assert(kInstrPerWave >= 1 && kChunksPerRow >= 8, "tile must split over four waves");
+    static_assert(kInstrPerWave >= 1 && kChunksPerRow >= 16, "tile must split over four waves");
 #pragma unroll
     for (int j = 0; j < kInstrPerWave; ++j) {
         const int slot0 = (wave * kInstrPerWave + j) * 64;
         const int slot = slot0 + lane;
         const int row = slot / kChunksPerRow;
-        const int chunk = (slot % kChunksPerRow) ^ (row & 7);
+        const int chunk = (slot % kChunksPerRow) ^ (row & 15);
         uint64_t key = k0 + row;
         if (k0 + 32 > rows && key >= rows) key = rows - 1;  // only the last tile clamps
         const float* src = g + key * ld + chunk * 4;
@@ -133,7 +136,7 @@ __device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
     const float* krow = sk + l32 * D;
-    const int swz = l32 & 7;
+    const int swz = l32 & 15;
 #pragma unroll
     for (int t = 0; t < D / 2; t += 4) {
         const int chunk = (half * (D / 8) + t / 4) ^ swz;
@@ -249,7 +252,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
     auto load_v = [&](uint64_t k0, float* dst) { dma_tile<VD>(V, v_ld, k0, a.kv_seq, dst, wave, lane); };
 
     // V reads: key row `key`, column vb*32 + l32 sits in chunk
-    // (vb*8 + l32/4) ^ (key & 7); key & 7 = 4*half + t%4 for step t.
+    // (vb*8 + l32/4) ^ (key & 15), and key & 15 = 8*((t/4) & 1) + 4*half +
+    // t%4 for step t: block vb ^ ((t/4) & 1), chunk (l32/4) ^ (4*half + t%4).
     int vx[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) vx[j] = (((l32 >> 2) ^ (4 * half + j)) << 2) + (l32 & 3);
@@ -327,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
                     const int key_row = 8 * (t / 4) + 4 * half + (t % 4);
-                    const float v = sv[key_row * VD + vb * 32 + vx[t % 4]];
+                    const float v = sv[key_row * VD + (vb ^ ((t >> 2) & 1)) * 32 + vx[t % 4]];
                     o[vb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, s_cur[t], o[vb], 0, 0, 0);
                 }
             }
