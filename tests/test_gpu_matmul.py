@@ -254,3 +254,28 @@ def test_large_tile_path_with_transposed_operands(dev, orc, ta, tb):
     assert max_normwise_err(got, want) <= TOL
     plain = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
+
+
+def _offset_view(dev, host):
+    """`host` on the device 4 bytes past a 16-byte boundary (and the owner to keep alive)."""
+    from magnetar_hip.device import DeviceArray
+    owner = dev.upload(np.concatenate([np.zeros(1, np.float32), host.ravel()]))
+    return DeviceArray(dev, owner.ptr + 4, host.shape, np.float32, owned=False), owner
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", [(512, 256, 512, False, False), (512, 256, 512, True, True),
+                                         (256, 160, 384, False, True), (96, 200, 160, False, False)])
+def test_unaligned_operands_give_the_aligned_bits(dev, orc, m, k, n, ta, tb):
+    """Misaligned operands take the register-staged slices (bounds-checked
+    scalar loads), aligned ones the direct global-to-LDS slices; both sum k
+    in the same order, so the products are bit-identical."""
+    from magnetar_hip import ops
+    a = orc.normal(m * k, 301).reshape((k, m) if ta else (m, k))
+    b = orc.normal(k * n, 302).reshape((n, k) if tb else (k, n))
+    aligned = ops.matmul(dev, dev.upload(a), dev.upload(b), ta, tb).numpy()
+    av, a_owner = _offset_view(dev, a)
+    bv, b_owner = _offset_view(dev, b)
+    shifted = ops.matmul(dev, av, bv, ta, tb).numpy()
+    assert_bitexact(shifted, aligned)
+    ref, _ = orc.matmul(a, b, ta, tb)
+    assert max_normwise_err(aligned, ref) < TOL
