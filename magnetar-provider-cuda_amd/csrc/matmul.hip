@@ -259,25 +259,35 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     float4 ra[Cfg::kAChunks], rb[Cfg::kBChunks];
     const bool interior_tile = VEC && m0 + BM <= M && n0 + BN <= N;
     auto direct = [&](uint64_t k0) { return interior_tile && k0 + BK <= k_end; };
+    // The direct loads of a slice are all issued by the first half of the
+    // waves: the older wave on each SIMD, which wins MFMA arbitration and
+    // otherwise finishes its share of the slice first and waits at the
+    // barrier; the younger one starts its MFMAs at once. Measured: 4096^3
+    // 87.4-88.3 -> 88.3-88.9 %, 8192^3 89.1 -> 89.8 %.
+    constexpr int kDmaWaves = Cfg::kWaves / 2;
     auto issue = [&](uint64_t k0, int buf) {
         float* la = lds + buf * Cfg::kLdsA;
         float* lb = lds_b0 + buf * Cfg::kLdsB;
         if (direct(k0)) {
-            if constexpr (A_T)
-                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, M, k0, m0, la, wave, lane);
-            else
-                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, K, m0, k0, la, wave, lane);
-            if constexpr (kBDma) {
-                if constexpr (B_T)
-                    dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
-                        reinterpret_cast<const float*>(B), K, n0, k0, lb, wave, lane);
+            if (wave < kDmaWaves) {
+                if constexpr (A_T)
+                    dma_slice<Cfg::kARows, Cfg::kACols, kDmaWaves, kASwz>(A, M, k0, m0, la, wave, lane);
                 else
-                    dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
-                        reinterpret_cast<const float*>(B), N, k0, n0, lb, wave, lane);
-            } else if constexpr (B_T) {
-                load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, K, n0, k0);
-            } else {
-                load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, N, k0, n0);
+                    dma_slice<Cfg::kARows, Cfg::kACols, kDmaWaves, kASwz>(A, K, m0, k0, la, wave, lane);
+                if constexpr (kBDma) {
+                    if constexpr (B_T)
+                        dma_slice<Cfg::kBRows, Cfg::kBCols, kDmaWaves, kBSwz>(
+                            reinterpret_cast<const float*>(B), K, n0, k0, lb, wave, lane);
+                    else
+                        dma_slice<Cfg::kBRows, Cfg::kBCols, kDmaWaves, kBSwz>(
+                            reinterpret_cast<const float*>(B), N, k0, n0, lb, wave, lane);
+                }
+            }
+            if constexpr (!kBDma) {
+                if constexpr (B_T)
+                    load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, K, n0, k0);
+                else
+                    load_slice_interior<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T>(rb, B, N, k0, n0);
             }
             return;
         }
