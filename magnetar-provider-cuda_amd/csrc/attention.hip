@@ -140,11 +140,14 @@ __device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D
 #pragma unroll
     for (int t = 0; t < D / 2; t += 4) {
         const int chunk = (half * (D / 8) + t / 4) ^ swz;
-        const float4 kv = *reinterpret_cast<const float4*>(krow + chunk * 4);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[t], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[t + 1], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[t + 2], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[t + 3], s, 0, 0, 0);
+        // A native vector read: read through HIP's float4 struct, the compiler
+        // waited for the next tile's direct loads (vmcnt(0)) before the first
+        // score read, though they fill the other buffer.
+        const mhip::f32x4 kv = *reinterpret_cast<const mhip::f32x4*>(krow + chunk * 4);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[0], qf[t], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[1], qf[t + 1], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[2], qf[t + 2], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[3], qf[t + 3], s, 0, 0, 0);
     }
     return s;
 }
@@ -279,13 +282,14 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
     __syncthreads();
     for (int i = i_begin; i < i_end; ++i) {
         const int j = i - i_begin;
+        const int cur = j & 1;
         const uint64_t k0 = tile_begin + static_cast<uint64_t>(i) * Cfg::kBKV;
         if (i + 1 < i_end) {
-            load_k(k0 + Cfg::kBKV, kbuf(j + 1));
-            load_v(k0 + Cfg::kBKV, vbuf(j + 1));
+            load_k(k0 + Cfg::kBKV, kbuf(cur ^ 1));
+            load_v(k0 + Cfg::kBKV, vbuf(cur ^ 1));
         }
         if (wave_in(k0)) {
-            v16f s_cur = tile_scores<D>(kbuf(j), qf, l32, half);
+            v16f s_cur = tile_scores<D>(kbuf(cur), qf, l32, half);
             // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q; bit
             // j of `admit` says whether tile key j is admitted.
             // A tile every query of the wave admits whole needs no mask.
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
             const float keep = (psum == 0.0f && alpha == 1.0f) || l_new == 0.0f ? 1.0f : (l * alpha) * inv;
 #pragma unroll
             for (int r = 0; r < 16; ++r) s_cur[r] *= inv;
-            const float* sv = vbuf(j);
+            const float* sv = vbuf(cur);
 #pragma unroll
             for (int vb = 0; vb < VD / 32; ++vb) {
 #pragma unroll
