@@ -231,6 +231,26 @@ def _device_normal(dev, shape, s, std, bf16=False):
     return arr
 
 
+def selection_cases(dev, orc):
+    """Two decode-step helpers: greedy selection over a Llama-2 vocabulary
+    row and one K/V row appended in place (kv-write). Both are launch-bound;
+    their bytes are reported for completeness. Greedy selection returns its
+    column to the host (as the reference does), so each call's time includes
+    that 8-byte download and its synchronisation."""
+    from magnetar_hip import ops
+    cases = []
+    vocab = 32000
+    logits = dev.upload(orc.normal(vocab, seed(5, 40)).reshape(1, vocab))
+    cases.append(Case("greedy_select_32000", lambda i: ops.greedy_select(dev, logits, 0),
+                      vocab * 4, "hbm", [1, vocab]))
+    width, capacity = 4096, 2048
+    store = dev.empty((capacity, width))
+    row = dev.upload(orc.normal(width, seed(5, 41)).reshape(1, width))
+    cases.append(Case("kv_write_1x4096", lambda i: ops.kv_write(dev, store, row, i % capacity),
+                      2 * width * 4, "hbm", [1, width]))
+    return cases
+
+
 def decoder_cases(dev, orc):
     """The chained decoder block: config 0 (tiny, seq 32) and config 4
     (Llama-2-7B shapes: prefill 512, decode one token at KV 2048)."""
@@ -401,8 +421,10 @@ def main(argv=None):
     if wanted("attention"):
         cases += attention_cases(dev, orc)
     if not only or only - {c for c in only if c.startswith(("matmul", "attention", "decoder",
-                                                             "calibration"))}:
+                                                             "calibration", "greedy", "kv_write"))}:
         cases += streaming_cases(dev, orc)
+    if wanted("greedy") or wanted("kv_write"):
+        cases += selection_cases(dev, orc)
     if wanted("decoder"):
         cases += decoder_cases(dev, orc)
     if any(name.startswith("calibration") for name in only):
