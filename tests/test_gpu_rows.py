@@ -237,3 +237,18 @@ def test_rope_baseline_shape(dev, orc):
     err = rope_pair_err(x, got, want, p)
     print(f"rope [8192,4096]: max pair-relative err {err:.3e}")
     assert err <= ROPE_TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (8195, 2048), (9000, 1024)])
+def test_rmsnorm_many_rows_match_few_rows_bits(dev, orc, rows, cols):
+    """Many rows with one shared gain may take a kernel that normalises several
+    rows per workgroup; every row must still get the bits a call on that row
+    alone produces (same per-row reduction order)."""
+    from magnetar_hip import ops
+    x = orc.normal(rows * cols, 801 + cols).reshape(rows, cols)
+    w = orc.normal(cols, 802, 1.0, 0.1)
+    dw = dev.upload(w)
+    got = ops.rmsnorm(dev, dev.upload(x), dw, 1e-5).numpy()
+    for r0 in (0, 1, rows // 2 + 1, rows - 3):
+        part = ops.rmsnorm(dev, dev.upload(np.ascontiguousarray(x[r0:r0 + 3])), dw, 1e-5).numpy()
+        assert_bitexact(got[r0:r0 + 3], part)
