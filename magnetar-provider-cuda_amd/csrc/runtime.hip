@@ -99,9 +99,13 @@ struct mhip_graph {
 
 namespace {
 
-__global__ void set_word_kernel(uint64_t* word, uint64_t value) { *word = value; }
-
-__global__ void clear_flags_kernel(uint32_t* flags) { flags[threadIdx.x] = 0u; }
+// Ahead of every replay of a captured step: its offset word, and the failure
+// flags cleared (the step's launches then only ever set them). One launch,
+// not a graph node: the graph holds the step's own work only.
+__global__ void replay_prologue_kernel(uint64_t* word, uint64_t value, uint32_t* flags) {
+    if (threadIdx.x == 0) *word = value;
+    flags[threadIdx.x] = 0u;
+}
 
 }  // namespace
 
@@ -346,10 +350,7 @@ mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing) {
     ctx->capture_offset = offset;
     ctx->max_offset = UINT64_MAX;
     ctx->capture_failure.clear();
-    // The step's first work: clear the failure flags, which its launches
-    // then only ever set (a kernel, not a memset node).
-    hipLaunchKernelGGL(clear_flags_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->flags);
-    return mhip::check_launch("clearing the failure flags");
+    return MHIP_OK;
 }
 
 // Ends capture mode on the stream; returns the captured graph (or null).
@@ -371,7 +372,7 @@ mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offs
     std::string failure = ctx->capture_failure;
     size_t nodes = 0;
     if (failure.empty() && !graph) failure = "the step capture met a driver error";
-    if (failure.empty() && (hipGraphGetNodes(graph, nullptr, &nodes) != hipSuccess || nodes <= 1))
+    if (failure.empty() && (hipGraphGetNodes(graph, nullptr, &nodes) != hipSuccess || nodes == 0))
         failure = "the step capture recorded no work";
     hipGraphExec_t exec = nullptr;
     if (failure.empty()) {
@@ -419,8 +420,10 @@ mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset) {
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
                           "offset " + std::to_string(offset) + " leaves the captured bounds (at most " +
                               std::to_string(graph->max_offset) + ")");
-    // The offset is written by a kernel on the same stream, ahead of the graph.
-    hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
+    // The offset is written, and the flags cleared, by a kernel on the same
+    // stream, ahead of the graph.
+    hipLaunchKernelGGL(replay_prologue_kernel, dim3(1), dim3(64), 0, ctx->stream, graph->offset,
+                       offset, ctx->flags);
     mhip_status st = mhip::check_launch("writing the replay offset");
     if (st != MHIP_OK) return st;
     return mhip::from_hip(hipGraphLaunch(graph->exec, ctx->stream), "launching a captured step");
