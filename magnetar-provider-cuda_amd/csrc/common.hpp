@@ -16,6 +16,11 @@ struct mhip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     uint32_t* flags = nullptr;  // device word, bits MHIP_FLAG_*
+    // Greedy selection: a device key word and workgroup counter, zero between
+    // calls (each call's last workgroup resets them), and a pinned host word
+    // the last workgroup writes the answer into.
+    uint64_t* select_state = nullptr;
+    uint64_t* select_host = nullptr;
     hipEvent_t timer_start = nullptr;
     hipEvent_t timer_stop = nullptr;
     uint32_t compute_units = 0;

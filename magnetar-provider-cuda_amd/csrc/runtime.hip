@@ -160,7 +160,12 @@ mhip_status mhip_ctx_create(int ordinal, mhip_ctx** out) {
     if ((err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
         (err = hipMalloc(reinterpret_cast<void**>(&ctx->flags), 256)) != hipSuccess ||
         (err = hipMemset(ctx->flags, 0, 256)) != hipSuccess ||
-
+        (err = hipMalloc(reinterpret_cast<void**>(&ctx->select_state), 256)) != hipSuccess ||
+        (err = hipMemset(ctx->select_state, 0, 256)) != hipSuccess ||
+        (err = hipHostMalloc(reinterpret_cast<void**>(&ctx->select_host), 256,
+                             hipHostMallocCoherent)) != hipSuccess ||
+        // The context's stream does not wait for the null stream's memsets.
+        (err = hipDeviceSynchronize()) != hipSuccess ||
         (err = hipEventCreate(&ctx->timer_start)) != hipSuccess ||
         (err = hipEventCreate(&ctx->timer_stop)) != hipSuccess) {
         mhip_status st = mhip::from_hip(err, "creating the device context");
@@ -177,6 +182,8 @@ mhip_status mhip_ctx_destroy(mhip_ctx* ctx) {
     mhip_capture_abort(ctx);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->flags) (void)hipFree(ctx->flags);
+    if (ctx->select_state) (void)hipFree(ctx->select_state);
+    if (ctx->select_host) (void)hipHostFree(ctx->select_host);
     for (auto& table : ctx->rope_tables) (void)hipFree(table.device);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
     // Graphs not destroyed by now can no longer run: their buffers go too.

@@ -8,8 +8,14 @@
 // Each eligible column becomes one 64-bit key: the score's bits mapped so
 // that unsigned order is float order, above the complement of the column.
 // The largest key names the answer whatever order workgroups finish in, so
-// a grid-wide atomic max over per-workgroup maxima is deterministic. Only the
-// 8-byte key comes back to the host.
+// a grid-wide atomic max over per-workgroup maxima is deterministic.
+//
+// One launch does the whole call: each workgroup folds its maximum into the
+// context's device key word and then counts itself in with a wrapping
+// increment; the workgroup that counts last swaps the key back to zero (the
+// counter has wrapped to zero by itself) and stores the key into a pinned
+// host word with a system-scope store, so the host only synchronises and
+// reads 8 bytes: no clearing launch and no copy.
 #include "common.hpp"
 
 namespace {
@@ -23,12 +29,11 @@ __device__ __forceinline__ uint64_t column_key(float value, uint64_t column) {
     return (static_cast<uint64_t>(ordered) << 32) | (0xFFFFFFFFull - (column & 0xFFFFFFFFull));
 }
 
-__global__ void clear_key_kernel(unsigned long long* best) { *best = 0ull; }
-
 __global__ __launch_bounds__(kThreads) void greedy_select_kernel(
     const float* __restrict__ row, uint64_t cols, const uint64_t* __restrict__ ranges,
-    uint32_t range_count, float temperature, unsigned long long* best) {
+    uint32_t range_count, float temperature, unsigned long long* state, uint64_t* host) {
     __shared__ unsigned long long wave_best[kThreads / 64];
+    __shared__ bool last;
     uint64_t key = 0;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < cols; i += stride) {
@@ -53,7 +58,16 @@ __global__ __launch_bounds__(kThreads) void greedy_select_kernel(
     if (threadIdx.x == 0) {
         uint64_t k = wave_best[0];
         for (int w = 1; w < kThreads / 64; ++w) k = wave_best[w] > k ? wave_best[w] : k;
-        if (k != 0) atomicMax(best, static_cast<unsigned long long>(k));
+        if (k != 0) atomicMax(&state[0], static_cast<unsigned long long>(k));
+        __threadfence();  // the maximum lands before this workgroup counts in
+        auto* counter = reinterpret_cast<unsigned int*>(&state[1]);
+        last = atomicInc(counter, gridDim.x - 1) == gridDim.x - 1;
+        if (last) {
+            __threadfence();  // every other workgroup's maximum is visible
+            const unsigned long long best = atomicExch(&state[0], 0ull);
+            __hip_atomic_store(host, static_cast<uint64_t>(best), __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
@@ -75,28 +89,33 @@ extern "C" mhip_status mhip_greedy_select_f32(mhip_ctx* ctx, const float* logits
     // The answer is downloaded, so the call cannot be captured.
     if (mhip_status st = mhip::forbid_in_capture(ctx, "a device-to-host download"); st != MHIP_OK)
         return st;
-    // Scratch: the key word, then the excluded ranges.
-    void* scratch = nullptr;
-    const size_t bytes = 256 + static_cast<size_t>(range_count) * 2 * sizeof(uint64_t);
-    mhip_status st = mhip::workspace(ctx, bytes, &scratch);
-    if (st != MHIP_OK) return st;
-    auto* best = static_cast<unsigned long long*>(scratch);
-    uint64_t* ranges = reinterpret_cast<uint64_t*>(static_cast<char*>(scratch) + 256);
-    hipError_t err = hipSuccess;
-    if (range_count)
-        err = hipMemcpyAsync(ranges, excluded, static_cast<size_t>(range_count) * 2 * sizeof(uint64_t),
-                             hipMemcpyHostToDevice, ctx->stream);
-    if (err != hipSuccess) return mhip::from_hip(err, "uploading the excluded ranges");
-    hipLaunchKernelGGL(clear_key_kernel, dim3(1), dim3(1), 0, ctx->stream, best);
+    // The excluded ranges go to the workspace; the key and counter live in
+    // the context, zero between calls.
+    uint64_t* ranges = nullptr;
+    if (range_count) {
+        void* scratch = nullptr;
+        mhip_status st = mhip::workspace(ctx, static_cast<size_t>(range_count) * 2 * sizeof(uint64_t),
+                                         &scratch);
+        if (st != MHIP_OK) return st;
+        ranges = static_cast<uint64_t*>(scratch);
+        hipError_t err = hipMemcpyAsync(ranges, excluded,
+                                        static_cast<size_t>(range_count) * 2 * sizeof(uint64_t),
+                                        hipMemcpyHostToDevice, ctx->stream);
+        if (err != hipSuccess) return mhip::from_hip(err, "uploading the excluded ranges");
+    }
+    volatile uint64_t* answer = ctx->select_host;
+    *answer = ~0ull;
     const uint64_t blocks = std::min<uint64_t>(256, (cols + 4 * kThreads - 1) / (4 * kThreads));
     hipLaunchKernelGGL(greedy_select_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                       ctx->stream, logits + row * cols, cols, ranges, range_count, temperature, best);
-    st = mhip::check_launch("greedy selection");
+                       ctx->stream, logits + row * cols, cols, ranges, range_count, temperature,
+                       reinterpret_cast<unsigned long long*>(ctx->select_state), ctx->select_host);
+    mhip_status st = mhip::check_launch("greedy selection");
     if (st != MHIP_OK) return st;
-    uint64_t key = 0;
-    err = hipMemcpyAsync(&key, best, sizeof(key), hipMemcpyDeviceToHost, ctx->stream);
-    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    const hipError_t err = hipStreamSynchronize(ctx->stream);
     if (err != hipSuccess) return mhip::from_hip(err, "reading the greedy selection");
+    const uint64_t key = *answer;
+    if (key == ~0ull)
+        return mhip::fail(MHIP_EXECUTION_FAILED, "greedy selection: the kernel left no answer");
     if (key != 0) *column = static_cast<int64_t>(0xFFFFFFFFull - (key & 0xFFFFFFFFull));
     return MHIP_OK;
 }
