@@ -235,7 +235,9 @@ mhip_status mhip_embedding_bf16w_f32(mhip_ctx* ctx, const uint16_t* table, uint6
  * as is when temperature is 0) among finite scores outside the `range_count`
  * excluded [start, end) pairs in `excluded` (host memory, 2 * range_count
  * values); ties go to the lowest column. *column = -1 when no column is
- * eligible. Downloads 8 bytes. */
+ * eligible. One kernel launch; the answer arrives in a pinned host word of
+ * the context and the call synchronises the context's stream. Calls on one
+ * context must not overlap (they share that word and the device key). */
 mhip_status mhip_greedy_select_f32(mhip_ctx* ctx, const float* logits, uint64_t rows,
                                    uint64_t cols, uint64_t row, const uint64_t* excluded,
                                    uint32_t range_count, float temperature, int64_t* column);
