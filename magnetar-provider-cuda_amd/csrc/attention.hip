@@ -25,8 +25,9 @@
 //    never overflows (the reference's 1e38 known answer,
 //    src/tests_conformance.rs:2215-2312).
 //  - decode (one query row, head dim 4, 8, 16, ..., 256): split-KV. A
-//    workgroup takes one (batch, KV head, key chunk) and all the query heads
-//    that share that KV head, issues every K and V load of the chunk at once
+//    workgroup takes one (batch, KV head, key chunk) and the query heads
+//    that share that KV head (up to 8; a larger group is split into slices
+//    of 8, each reading the chunk), issues every K and V load of the chunk at once
 //    (non-temporal dwordx4), keeps scores and probabilities in registers, and
 //    writes the chunk's normalised output, max and weight sum; a second
 //    kernel merges the chunks in a fixed order (deterministic).
@@ -419,6 +420,9 @@ void prefill_split(const mhip_ctx* ctx, const AttnArgs& a, uint64_t qtiles, uint
                    uint32_t* nchunks, uint32_t* chunk_tiles) {
     *nchunks = 1;
     *chunk_tiles = 0;
+    // A replayed key count may pass the captured one: chunks sized here from
+    // the captured count would leave the later keys to no workgroup.
+    if (a.advance) return;
     const uint64_t slots = 2 * static_cast<uint64_t>(ctx->compute_units ? ctx->compute_units : 256);
     const uint64_t per_sequence = a.heads * qtiles;
     const uint64_t kv_tiles = (a.kv_seq + kbkv - 1) / kbkv;
@@ -470,7 +474,7 @@ mhip_status launch_prefill(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
 // Decode: split-KV over key chunks, all query heads of a KV head together
 // ---------------------------------------------------------------------------
 
-constexpr int kMaxGroup = 8;
+constexpr int kMaxGroup = 8;  // query heads per workgroup; larger groups take several
 
 // Keys per chunk for head dim 4*D4: kDecodeSteps(D4) steps of 256/D4 keys
 // (D4 lanes hold one key row, 64/D4 keys per wave, four waves). At D >= 16
@@ -499,12 +503,19 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 
     // (batch, KV head) varies fastest: workgroups in flight together read
     // whole K/V rows (all heads of the same keys) rather than one head's
-    // 4*D-byte slice of many rows.
-    const int group = static_cast<int>(a.heads / a.kv_heads);
+    // 4*D-byte slice of many rows. A group of more than GT query heads is
+    // taken GT heads at a time (head slice hs), each slice reading the chunk.
+    const int group_all = static_cast<int>(a.heads / a.kv_heads);
+    const int slices = (group_all + GT - 1) / GT;
     const uint64_t units = gridDim.x / chunks;
     const uint64_t c_idx = blockIdx.x / units;
-    const uint64_t bkv = blockIdx.x % units;
+    const uint64_t unit = blockIdx.x % units;
+    const uint64_t pairs = units / static_cast<uint64_t>(slices);
+    const int hs = static_cast<int>(unit / pairs);
+    const uint64_t bkv = unit % pairs;
     const uint64_t kvh = bkv % a.kv_heads, b = bkv / a.kv_heads;
+    const int group = min(GT, group_all - hs * GT);
+    const uint64_t head0 = kvh * static_cast<uint64_t>(group_all) + static_cast<uint64_t>(hs) * GT;
     // The chunk's keys: [key_base + c * chunk, + chunk) inside the admitted
     // range of the query (at position offset; a replay may move it).
     apply_advance(a);
@@ -532,7 +543,7 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
             vr[u] = mhip::load_nt(reinterpret_cast<const float4*>(V + (c_lo + j) * k_ld));
         }
     }
-    const float* Qb = a.q + b * a.q_bs + kvh * static_cast<uint64_t>(group) * D;
+    const float* Qb = a.q + b * a.q_bs + head0 * D;
     for (int i = threadIdx.x; i < group * D4; i += 256) {
         float4 q4 = *reinterpret_cast<const float4*>(Qb + 4 * static_cast<uint64_t>(i));
         q4.x *= a.qscale; q4.y *= a.qscale; q4.z *= a.qscale; q4.w *= a.qscale;
@@ -606,7 +617,7 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
     __syncthreads();
 
-    const uint64_t bh0 = b * a.heads + kvh * static_cast<uint64_t>(group);
+    const uint64_t bh0 = b * a.heads + head0;
     for (int i = threadIdx.x; i < group * D4; i += 256) {
         const int g = i / D4, t = i % D4;
         float4 o = red[0][g][t];
@@ -724,7 +735,8 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
     }
     uint64_t chunks = (hi - lo + kChunk - 1) / kChunk;
     if (chunks == 0) chunks = 1;
-    const uint64_t units = batch * a.kv_heads;
+    const uint64_t slices = (a.heads / a.kv_heads + GT - 1) / GT;
+    const uint64_t units = batch * a.kv_heads * slices;
     if (units * chunks >= (1ULL << 31))
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention decode: too many key chunks");
     const uint64_t records = batch * a.heads * chunks;
@@ -753,7 +765,7 @@ mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch, uint
     if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch, kv_rows, bounded);
     if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch, kv_rows, bounded);
     if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch, kv_rows, bounded);
-    return launch_decode_group<D4, 8>(ctx, a, batch, kv_rows, bounded);
+    return launch_decode_group<D4, kMaxGroup>(ctx, a, batch, kv_rows, bounded);
 }
 
 // ---------------------------------------------------------------------------
@@ -888,8 +900,7 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
     const bool aligned = mhip::aligned16(q) && mhip::aligned16(k) && mhip::aligned16(v) &&
                          mhip::aligned16(out) && a.q_bs % 4 == 0 && a.k_bs % 4 == 0 &&
                          a.v_bs % 4 == 0 && a.o_bs % 4 == 0;
-    if (aligned && p->seq_len == 1 && vd == d && d % 4 == 0 && d <= 256 && H / Hkv <= kMaxGroup &&
-        p->kv_seq_len > 0) {
+    if (aligned && p->seq_len == 1 && vd == d && d % 4 == 0 && d <= 256 && p->kv_seq_len > 0) {
         mhip_status st = MHIP_CAPTURE_UNSUPPORTED;
         switch (d / 4) {
             case 1: st = launch_decode<1>(ctx, a, batch, p->kv_rows, p->bounded_key_count != 0); break;

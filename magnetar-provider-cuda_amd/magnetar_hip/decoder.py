@@ -112,32 +112,3 @@ class DecoderBlock:
             self.cache_rows, ctypes.c_void_p(self.ws.ptr), self.ws_bytes, ctypes.c_void_p(out.ptr)))
         return out
 
-
-def reference_block(orc, shapes: Shapes, weights: dict, ids, position: int, k_cache, v_cache):
-    """The same chain on the CPU oracle; returns (out, k_cache, v_cache) with the
-    new K/V rows written at `position`. Test/bench infrastructure only."""
-    s = shapes
-    x, st = orc.embedding(weights["embedding"], ids)
-    assert st == 0
-    h, _ = orc.rmsnorm(x, weights["attn_norm"], s.eps)
-    q, _ = orc.matmul(h, weights["wq"])
-    k, _ = orc.matmul(h, weights["wk"])
-    v, _ = orc.matmul(h, weights["wv"])
-    q, _ = orc.rope(q, orc.rope_params(s.head_dim, s.heads, base=s.rope_base, position_offset=position))
-    k, _ = orc.rope(k, orc.rope_params(s.head_dim, s.kv_heads, base=s.rope_base, position_offset=position))
-    seq = len(ids)
-    k_cache = k_cache.copy()
-    v_cache = v_cache.copy()
-    k_cache[position:position + seq] = k
-    v_cache[position:position + seq] = v
-    p = orc.attention_params(seq, k_cache.shape[0], s.heads, s.head_dim, kv_head_count=s.kv_heads,
-                             causal=True, key_count=position + seq)
-    a, st = orc.attention(q, k_cache, v_cache, p)
-    assert st == 0
-    x2, _ = orc.matmul(a, weights["wo"], addend=x, addend_mode=2)
-    h2, _ = orc.rmsnorm(x2, weights["ffn_norm"], s.eps)
-    g, _ = orc.matmul(h2, weights["w_gate"])
-    u, _ = orc.matmul(h2, weights["w_up"])
-    f, _ = orc.silu_mul(g, u)
-    out, _ = orc.matmul(f, weights["w_down"], addend=x2, addend_mode=2)
-    return out, k_cache, v_cache

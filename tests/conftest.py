@@ -63,3 +63,17 @@ def max_normwise_err(actual, expected) -> float:
         return 0.0
     scale = float(np.max(np.abs(e)))
     return float(np.max(np.abs(a - e))) / (scale if scale > 0 else 1.0)
+
+
+def max_rel_err_significant(actual, expected, frac: float = 1e-3) -> float:
+    """max_i |a_i - e_i| / |e_i| over the entries with |e_i| >= frac * max|e|:
+    the elementwise relative error where it is defined (an entry that cancels
+    to ~0 has none)."""
+    a = np.asarray(actual, np.float64).reshape(-1)
+    e = np.asarray(expected, np.float64).reshape(-1)
+    if a.size == 0:
+        return 0.0
+    keep = np.abs(e) >= frac * float(np.max(np.abs(e)))
+    if not keep.any():
+        return 0.0
+    return float(np.max(np.abs(a[keep] - e[keep]) / np.abs(e[keep])))

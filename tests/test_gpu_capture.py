@@ -11,6 +11,8 @@ is checked.
 import numpy as np
 import pytest
 
+from conftest import max_normwise_err, max_rel_err
+
 pytestmark = pytest.mark.gpu
 
 
@@ -40,7 +42,7 @@ def test_the_executor_supports_step_capture(ex):
     assert ex.supports_step_capture()
 
 
-def test_a_captured_step_replays_with_an_advanced_position(ex):
+def test_a_captured_step_replays_with_an_advanced_position(ex, orc):
     """src/tests_hardware_hot_path.rs:633-727: rope then rmsnorm, captured at
     position 3 and replayed at offset 4 with other inputs, equals the eager
     step at position 7."""
@@ -61,6 +63,12 @@ def test_a_captured_step_replays_with_an_advanced_position(ex):
     ex.write_tensor("replay.x", first)
     first_at_3 = step(3)
     assert not np.array_equal(first_at_3, second_at_7)
+    # The oracle's step at each position.
+    gain = np.array([0.5, 1.0, 1.5, 2.0], np.float32)
+    for x, position, got in ((first, 3, first_at_3), (second, 7, second_at_7)):
+        rotated, _ = orc.rope(x, orc.rope_params(4, 1, position_offset=position))
+        want, _ = orc.rmsnorm(rotated, gain, 1e-6)
+        assert max_rel_err(got, want) <= 1e-4, position
 
     ex.begin_step_capture(["position_offset"])
     step(3, read=False)
@@ -123,7 +131,7 @@ def _values(count, seed):
 
 
 @pytest.mark.parametrize("rows,head_dimension", [(16, 64), (32, 128), (8, 64)])
-def test_a_captured_prefill_attention_replays_at_its_key_count(ex, rows, head_dimension):
+def test_a_captured_prefill_attention_replays_at_its_key_count(ex, orc, rows, head_dimension):
     """src/tests_hardware_hot_path.rs:729-827: several query rows replay with new
     queries exactly like an eager dispatch, and only at offset 0."""
     from magnetar_hip import Integer, KernelError
@@ -147,6 +155,13 @@ def test_a_captured_prefill_attention_replays_at_its_key_count(ex, rows, head_di
     attention()
     expected_first = ex.read_tensor(pre + ".out")
     assert not np.array_equal(expected_first, expected_second)
+    k_host = _values(capacity * width, 3).reshape(capacity, width)
+    v_host = _values(capacity * width, 4).reshape(capacity, width)
+    ap = orc.attention_params(rows, capacity, 2, head_dimension, causal=True, key_count=rows)
+    for q_host, got in ((first, expected_first), (second, expected_second)):
+        want, st = orc.attention(q_host, k_host, v_host, ap)
+        assert st == 0
+        assert max_normwise_err(got, want) <= 1e-4
 
     ex.begin_step_capture(["key_count"])
     attention()
@@ -163,86 +178,159 @@ def test_a_captured_prefill_attention_replays_at_its_key_count(ex, rows, head_di
     ex.release_step_capture(capture)
 
 
-@pytest.mark.parametrize("heads,kv_heads,dim", [(4, 4, 64), (8, 2, 128), (2, 1, 4)])
-def test_a_captured_decode_step_advances_position_cache_row_and_key_count(ex, orc, heads,
-                                                                          kv_heads, dim):
-    """A decode step -- RoPE on q and k at position p, kv-write of k and v at row
-    p, attention over key_count p + 1 -- captured at p = 0 and replayed at
-    offset t equals the eager step at p = t, outputs and cache rows."""
-    from magnetar_hip import Integer
-    steps, capacity = 6, 40
-    qw, kw = heads * dim, kv_heads * dim
-    pre = f"dec.{heads}.{kv_heads}.{dim}"
-    q_in = [orc.normal(qw, 10 + t).reshape(1, qw) for t in range(steps)]
-    k_in = [orc.normal(kw, 30 + t).reshape(1, kw) for t in range(steps)]
-    v_in = [orc.normal(kw, 50 + t).reshape(1, kw) for t in range(steps)]
+def _rope_pair_err(got, want):
+    """Largest |got - want| over each rotated pair, relative to the pair's norm
+    (RoPE's bar: a rotation keeps the pair's norm, whatever its angle)."""
+    g = np.asarray(got, np.float64).reshape(-1, 2)
+    w = np.asarray(want, np.float64).reshape(-1, 2)
+    norm = np.maximum(np.hypot(w[:, 0], w[:, 1]), 1e-30)
+    return float(np.max(np.hypot(*(g - w).T) / norm)) if g.size else 0.0
 
-    def step(t, read=True):
-        rope = {"dimension": Integer(dim), "position_offset": Integer(t)}
+
+DECODE_CASES = [
+    # heads, kv_heads, dim, first position, capacity, replay offsets
+    (4, 4, 64, 0, 40, (0, 1, 2, 3, 4, 5)),
+    (8, 2, 128, 0, 40, (0, 1, 2, 3, 4, 5)),
+    (2, 1, 4, 0, 40, (0, 1, 2, 3, 4, 5)),
+    # More than 8 query heads per KV head, captured past 256 keys and replayed
+    # far past the captured count (keys the capture-time split never saw).
+    (32, 2, 128, 300, 512, (0, 1, 37, 100, 180, 211)),
+    (16, 1, 64, 260, 640, (0, 5, 120, 379)),
+    (12, 1, 128, 257, 400, (0, 64, 142)),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,dim,start,capacity,offsets", DECODE_CASES)
+def test_a_captured_decode_step_advances_position_cache_row_and_key_count(
+        ex, orc, heads, kv_heads, dim, start, capacity, offsets):
+    """A decode step -- RoPE on q and k at position p, kv-write of k and v at row
+    p, attention over key_count p + 1 -- captured at p = start and replayed at
+    offset t equals the eager step at p = start + t (outputs and cache rows,
+    bit for bit) and the oracle's step at that position: RoPE at p + t, the
+    rows written into a host copy of the cache, attention over the cache's
+    first p + t + 1 rows."""
+    from magnetar_hip import Integer
+    qw, kw = heads * dim, kv_heads * dim
+    pre = f"dec.{heads}.{kv_heads}.{dim}.{start}"
+    n = len(offsets)
+    q_in = [orc.normal(qw, 10 + t).reshape(1, qw) for t in range(n)]
+    k_in = [orc.normal(kw, 30 + t).reshape(1, kw) for t in range(n)]
+    v_in = [orc.normal(kw, 50 + t).reshape(1, kw) for t in range(n)]
+    history_k = np.zeros((capacity, kw), np.float32)
+    history_v = np.zeros((capacity, kw), np.float32)
+    history_k[:start] = orc.normal(start * kw, 70, 0.0, 0.5).reshape(start, kw)
+    history_v[:start] = orc.normal(start * kw, 71, 0.0, 0.5).reshape(start, kw)
+
+    def stores():
+        if start:
+            ex.write_tensor(pre + ".kc", history_k)
+            ex.write_tensor(pre + ".vc", history_v)
+        else:
+            assert ex.write_zeroed_kv_store(pre + ".kc", (capacity, kw))
+            assert ex.write_zeroed_kv_store(pre + ".vc", (capacity, kw))
+
+    def step(p, read=True):
+        rope = {"dimension": Integer(dim), "position_offset": Integer(p)}
         ex.execute(inv("rope", [pre + ".q"], pre + ".qr", dict(rope, head_count=Integer(heads))))
         ex.execute(inv("rope", [pre + ".k"], pre + ".kr", dict(rope, head_count=Integer(kv_heads))))
-        ex.execute(inv("kv-write", [pre + ".kc", pre + ".kr"], pre + ".kc", {"row_offset": Integer(t)}))
-        ex.execute(inv("kv-write", [pre + ".vc", pre + ".v"], pre + ".vc", {"row_offset": Integer(t)}))
+        ex.execute(inv("kv-write", [pre + ".kc", pre + ".kr"], pre + ".kc", {"row_offset": Integer(p)}))
+        ex.execute(inv("kv-write", [pre + ".vc", pre + ".v"], pre + ".vc", {"row_offset": Integer(p)}))
         ex.execute(inv("attention", [pre + ".qr", pre + ".kc", pre + ".vc"], pre + ".out",
                        {"head_count": Integer(heads), "head_dimension": Integer(dim),
                         "kv_head_count": Integer(kv_heads), "causal": True,
-                        "key_count": Integer(t + 1)}))
+                        "key_count": Integer(p + 1)}))
         if read:
             return ex.read_tensor(pre + ".out"), ex.read_tensor(pre + ".kc"), ex.read_tensor(pre + ".vc")
 
-    # Eager reference.
-    assert ex.write_zeroed_kv_store(pre + ".kc", (capacity, kw))
-    assert ex.write_zeroed_kv_store(pre + ".vc", (capacity, kw))
-    eager = []
-    for t in range(steps):
-        ex.write_tensor(pre + ".q", q_in[t])
-        ex.write_tensor(pre + ".k", k_in[t])
-        ex.write_tensor(pre + ".v", v_in[t])
-        eager.append(step(t))
+    def inputs(i):
+        ex.write_tensor(pre + ".q", q_in[i])
+        ex.write_tensor(pre + ".k", k_in[i])
+        ex.write_tensor(pre + ".v", v_in[i])
 
-    # Fresh caches; one eager step creates the outputs, then capture at p = 0.
-    assert ex.write_zeroed_kv_store(pre + ".kc", (capacity, kw))
-    assert ex.write_zeroed_kv_store(pre + ".vc", (capacity, kw))
-    ex.write_tensor(pre + ".q", q_in[0])
-    ex.write_tensor(pre + ".k", k_in[0])
-    ex.write_tensor(pre + ".v", v_in[0])
-    step(0)
+    # The oracle's steps, on a host copy of the cache.
+    kc_host, vc_host = history_k.copy(), history_v.copy()
+    want = []
+    for i, t in enumerate(offsets):
+        p = start + t
+        qr, _ = orc.rope(q_in[i], orc.rope_params(dim, heads, position_offset=p))
+        kr, _ = orc.rope(k_in[i], orc.rope_params(dim, kv_heads, position_offset=p))
+        kc_host[p] = kr[0]
+        vc_host[p] = v_in[i][0]
+        ap = orc.attention_params(1, capacity, heads, dim, kv_head_count=kv_heads, causal=True,
+                                  key_count=p + 1)
+        out, st = orc.attention(qr, kc_host, vc_host, ap)
+        assert st == 0
+        want.append((out, kr[0].copy()))
+
+    # Eager steps at the same positions, in the same order.
+    stores()
+    eager = []
+    for i, t in enumerate(offsets):
+        inputs(i)
+        eager.append(step(start + t))
+
+    # Fresh stores; one eager step creates the outputs, then capture at p = start.
+    stores()
+    inputs(0)
+    step(start)
     ex.begin_step_capture(["position_offset", "row_offset", "key_count"])
-    step(0, read=False)
+    step(start, read=False)
     capture = ex.end_step_capture()
-    for t in range(steps):
-        if t:
-            ex.replay_step(capture, t, {pre + ".q": q_in[t], pre + ".k": k_in[t], pre + ".v": v_in[t]})
+    for i, t in enumerate(offsets):
+        if i:
+            ex.replay_step(capture, t, {pre + ".q": q_in[i], pre + ".k": k_in[i], pre + ".v": v_in[i]})
         out, kc, vc = (ex.read_tensor(pre + s) for s in (".out", ".kc", ".vc"))
-        assert np.array_equal(bits(out), bits(eager[t][0])), t
-        assert np.array_equal(bits(kc), bits(eager[t][1])), t
-        assert np.array_equal(bits(vc), bits(eager[t][2])), t
+        assert np.array_equal(bits(out), bits(eager[i][0])), t
+        assert np.array_equal(bits(kc), bits(eager[i][1])), t
+        assert np.array_equal(bits(vc), bits(eager[i][2])), t
+        err = max_normwise_err(out, want[i][0])
+        assert err <= 1e-4, (t, err)
+        assert _rope_pair_err(kc[start + t], want[i][1]) <= 1e-6, t
+        assert np.array_equal(bits(vc[start + t]), bits(v_in[i][0])), t
     ex.release_step_capture(capture)
 
 
-def test_a_captured_decoder_block_replays_decode_steps(dev, orc):
+BLOCK_CASES = [
+    # hidden, heads, kv_heads, head_dim, ffn, cache rows, position, replay offsets
+    (512, 8, 2, 64, 1024, 48, 20, (0, 1, 2, 3, 4)),
+    # 16 query heads per KV head, captured past 256 keys, replayed far past them.
+    (1024, 16, 1, 64, 1536, 420, 300, (0, 1, 57, 119)),
+]
+
+
+@pytest.mark.parametrize("hidden,heads,kv_heads,head_dim,ffn,rows,P,offsets", BLOCK_CASES)
+def test_a_captured_decoder_block_replays_decode_steps(dev, orc, hidden, heads, kv_heads,
+                                                       head_dim, ffn, rows, P, offsets):
     """mhip_block_forward captured once at position P (all three attributes
-    advancing) and replayed at offset t equals the eager block at P + t."""
+    advancing) and replayed at offset t equals the eager block at P + t bit
+    for bit, and the oracle's block at P + t within the block's 1e-4."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
     from magnetar_hip.device import (ADVANCE_KEY_COUNT, ADVANCE_POSITION_OFFSET,
                                      ADVANCE_ROW_OFFSET)
-    s = Shapes(vocab=512, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024)
+    from reference_chain import reference_block
+    s = Shapes(vocab=512, hidden=hidden, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=ffn)
     w = {}
     for i, (name, shape) in enumerate(s.weight_shapes().items()):
         n = int(np.prod(shape))
         w[name] = (orc.normal(n, 700 + i, 1.0, 0.1) if name.endswith("norm")
                    else orc.normal(n, 700 + i, 0.0, 0.02)).reshape(shape)
-    rows, P, steps = 48, 20, 5
-    history_k = orc.normal(rows * 128, 790, 0.0, 0.5).reshape(rows, 128)
-    history_v = orc.normal(rows * 128, 791, 0.0, 0.5).reshape(rows, 128)
-    ids = [orc.token_ids(1, 800 + t, 512) for t in range(steps)]
+    kw = kv_heads * head_dim
+    history_k = orc.normal(rows * kw, 790, 0.0, 0.5).reshape(rows, kw)
+    history_v = orc.normal(rows * kw, 791, 0.0, 0.5).reshape(rows, kw)
+    ids = [orc.token_ids(1, 800 + t, 512) for t in offsets]
 
     eager_block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1)
     eager_block.k_cache, eager_block.v_cache = dev.upload(history_k), dev.upload(history_v)
     eager = []
-    for t in range(steps):
-        out = eager_block.forward(dev.upload(ids[t]), P + t).numpy()
+    for i, t in enumerate(offsets):
+        out = eager_block.forward(dev.upload(ids[i]), P + t).numpy()
         eager.append((out, eager_block.k_cache.numpy(), eager_block.v_cache.numpy()))
+
+    kc_host, vc_host = history_k.copy(), history_v.copy()
+    want = []
+    for i, t in enumerate(offsets):
+        out, kc_host, vc_host = reference_block(orc, s, w, ids[i], P + t, kc_host, vc_host)
+        want.append(out)
 
     block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1)
     block.k_cache, block.v_cache = dev.upload(history_k), dev.upload(history_v)
@@ -253,12 +341,15 @@ def test_a_captured_decoder_block_replays_decode_steps(dev, orc):
     block.forward(ids_buf, P, out)
     graph = dev.capture_end()
     assert graph.max_offset == rows - (P + 1)
-    for t in range(steps):
-        dev.write(ids_buf, ids[t])
+    for i, t in enumerate(offsets):
+        dev.write(ids_buf, ids[i])
         graph.launch(t)
-        assert np.array_equal(bits(out.numpy()), bits(eager[t][0])), t
-        assert np.array_equal(bits(block.k_cache.numpy()), bits(eager[t][1])), t
-        assert np.array_equal(bits(block.v_cache.numpy()), bits(eager[t][2])), t
+        got = out.numpy()
+        assert np.array_equal(bits(got), bits(eager[i][0])), t
+        assert np.array_equal(bits(block.k_cache.numpy()), bits(eager[i][1])), t
+        assert np.array_equal(bits(block.v_cache.numpy()), bits(eager[i][2])), t
+        err = max_normwise_err(got, want[i])
+        assert err <= 1e-4, (t, err)
     import magnetar_hip
     with pytest.raises(magnetar_hip.MagnetarHipError):
         graph.launch(rows - P)  # past the cache

@@ -27,7 +27,8 @@ def weights_for(orc, shapes, seed=0):
 def test_tiny_block_prefill_and_decode(dev, orc):
     """Config 0: vocab 1024, hidden 256, 4 heads x 64, seq 32, FFN 688; then
     four decode steps appending to the cache."""
-    from magnetar_hip.decoder import DecoderBlock, Shapes, reference_block
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
     s = Shapes(vocab=1024, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=688)
     w = weights_for(orc, s, 100)
     block = DecoderBlock(dev, s, w, cache_rows=64, max_seq=32)
@@ -49,7 +50,8 @@ def test_tiny_block_prefill_and_decode(dev, orc):
 
 
 def test_gqa_block(dev, orc):
-    from magnetar_hip.decoder import DecoderBlock, Shapes, reference_block
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
     s = Shapes(vocab=512, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024, eps=1e-6,
                rope_base=500000.0)
     w = weights_for(orc, s, 200)
@@ -64,7 +66,8 @@ def test_gqa_block(dev, orc):
 def test_llama2_7b_block_decode_at_kv_2048(dev, orc):
     """Config 4 decode: hidden 4096, 32 x 128 heads, FFN 11008, one token at
     position 2048 against 2048 cached K/V rows."""
-    from magnetar_hip.decoder import DecoderBlock, Shapes, reference_block
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
     s = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     w = weights_for(orc, s, 300)
     rows = 2049
@@ -84,18 +87,23 @@ def test_llama2_7b_block_decode_at_kv_2048(dev, orc):
 
 
 def test_llama2_7b_block_prefill(dev, orc):
-    """Config 4 prefill shape at 64 tokens (the oracle's CPU time bounds the length)."""
-    from magnetar_hip.decoder import DecoderBlock, Shapes, reference_block
+    """Config 4 prefill: the BASELINE's 512 tokens at position 0 (hidden 4096,
+    32 x 128 heads, FFN 11008), output and the K/V rows the block writes."""
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
     s = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     w = weights_for(orc, s, 400)
-    block = DecoderBlock(dev, s, w, cache_rows=64, max_seq=64)
-    ids = orc.token_ids(64, 401, 32000)
+    seq = 512
+    block = DecoderBlock(dev, s, w, cache_rows=seq, max_seq=seq)
+    ids = orc.token_ids(seq, 401, 32000)
     got = block.forward(dev.upload(ids), 0).numpy()
-    want, _, _ = reference_block(orc, s, w, ids, 0, np.zeros((64, 4096), np.float32),
-                                 np.zeros((64, 4096), np.float32))
+    want, kc, vc = reference_block(orc, s, w, ids, 0, np.zeros((seq, 4096), np.float32),
+                                   np.zeros((seq, 4096), np.float32))
     err = max_normwise_err(got, want)
-    print(f"llama2-7b prefill(64): {err:.2e}")
-    assert err <= TOL
+    k_err = max_normwise_err(block.k_cache.numpy(), kc)
+    v_err = max_normwise_err(block.v_cache.numpy(), vc)
+    print(f"llama2-7b prefill(512): out {err:.2e}, K rows {k_err:.2e}, V rows {v_err:.2e}")
+    assert err <= TOL and k_err <= TOL and v_err <= TOL
 
 
 def _rows_view(arr, first, count):

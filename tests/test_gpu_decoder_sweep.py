@@ -26,7 +26,8 @@ def draw(seed):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_random_block(dev, orc, seed):
-    from magnetar_hip.decoder import DecoderBlock, Shapes, reference_block
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
     head_dim, heads, kv_heads, ffn, vocab, seq, position = draw(seed)
     hidden = heads * head_dim
     s = Shapes(vocab=vocab, hidden=hidden, heads=heads, kv_heads=kv_heads, head_dim=head_dim,

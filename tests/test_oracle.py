@@ -22,8 +22,12 @@ mistake (a dropped term, a wrong sign, index or operand order) would fail:
                     masked (-inf) entries; the all -inf failure
   rope              float64 textbook rotation on the reference's fixtures;
                     position 0 is the identity; pair norms preserved; half-split
-                    equals interleaved under the pair permutation; banded/YaRN
-                    frequency bands
+                    equals interleaved under the pair permutation; the banded
+                    (Llama 3.1) blend, the YaRN ramp, position scale and
+                    amplitude against independent float64 statements of their
+                    published definitions, each shown to fail on a planted
+                    mistake (swapped blend or ramp, divided scale, dropped
+                    amplitude)
   matmul            exact integer products; float64 brute force within the
                     gamma_k summation bound; transposes; fused addends
   attention         float64 textbook softmax(q k^T s + mask) v incl. GQA and
@@ -359,7 +363,215 @@ def test_rope_frequency_scaling_bands(orc):
     assert np.all(part[3:] == 0.0) and np.all(amp2[3:] == 1.0)
 
 
+# Independent float64 statements of the optional RoPE forms, from their
+# published definitions (not from the oracle's code):
+#  - Llama 3.1 banded scaling: with wavelength L_p = 2 pi / f_p and context
+#    length C, keep f_p when L_p < C / high, divide it by `factor` when
+#    L_p > C / low, and otherwise blend with s = (C / L_p - low) / (high - low):
+#    f' = (1 - s) f / factor + s f;
+#  - YaRN: ramp r_p = clamp((p - low) / (high - low), 0, 1) (high nudged by
+#    0.001 when equal to low), f' = r f / factor + (1 - r) f;
+#  - the position is (offset + row) * scale, the rotation angle position * f',
+#    and cos / sin are multiplied by `amplitude` on rotated pairs.
+# `mutant` plants one plausible mistake, to show the checks below catch it.
+
+def rope_freqs64(dim, base=10000.0, banded=None, yarn=None, rotated=None, mutant=None):
+    half = dim // 2
+    f = np.array([base ** (-2.0 * p / dim) for p in range(half)], np.float64)
+    if banded is not None:
+        factor, low, high, ctx = banded
+        out = f.copy()
+        for p in range(half):
+            wl = 2 * math.pi / f[p]
+            if wl < ctx / high:
+                continue
+            if wl > ctx / low:
+                out[p] = f[p] / factor
+            else:
+                sm = (ctx / wl - low) / (high - low)
+                if mutant == "swapped_blend":
+                    sm = 1.0 - sm
+                out[p] = (1 - sm) * f[p] / factor + sm * f[p]
+        f = out
+    if yarn is not None:
+        factor, low, high = yarn
+        hi = high + 0.001 if low == high else high
+        r = np.clip((np.arange(half) - low) / (hi - low), 0.0, 1.0)
+        if mutant == "swapped_ramp":
+            r = 1.0 - r
+        f = r * f / factor + (1 - r) * f
+    if rotated is not None:
+        f[rotated:] = 0.0
+    return f
+
+
+def rope_full64(x, dim, heads, offset, scale=1.0, amplitude=1.0, half_split=0, mutant=None,
+                **freq_kw):
+    x = np.asarray(x, np.float64)
+    rows, cols = x.shape
+    hw, half = cols // heads, dim // 2
+    f = rope_freqs64(dim, mutant=mutant, **freq_kw)
+    rotated = freq_kw.get("rotated")
+    amp = np.where(np.arange(half) < (rotated if rotated is not None else half), amplitude, 1.0)
+    if mutant == "dropped_amplitude":
+        amp = np.ones(half)
+    out = x.copy()
+    for r in range(rows):
+        pos = (offset + r) / scale if mutant == "divided_scale" else (offset + r) * scale
+        th = pos * f
+        c, sn = np.cos(th) * amp, np.sin(th) * amp
+        for h in range(heads):
+            p = np.arange(half)
+            i1 = h * hw + (p if half_split else 2 * p)
+            i2 = h * hw + (p + half if half_split else 2 * p + 1)
+            a, b = x[r, i1], x[r, i2]
+            out[r, i1] = a * c - b * sn
+            out[r, i2] = a * sn + b * c
+    return out
+
+
+def pair_err(got, want, dim, heads, half_split=0):
+    """Largest error of a rotated pair relative to the pair's norm."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    rows, cols = w.shape
+    hw, half = cols // heads, dim // 2
+    p = np.arange(half)
+    worst = 0.0
+    for h in range(heads):
+        i1 = h * hw + (p if half_split else 2 * p)
+        i2 = h * hw + (p + half if half_split else 2 * p + 1)
+        d = np.hypot(g[:, i1] - w[:, i1], g[:, i2] - w[:, i2])
+        n = np.maximum(np.hypot(w[:, i1], w[:, i2]), 1e-30)
+        worst = max(worst, float(np.max(d / n)))
+    return worst
+
+
+LLAMA31 = (8.0, 1.0, 4.0, 8192.0)        # factor, low, high, original context
+
+
+def test_rope_banded_frequencies_against_float64(orc):
+    """Every band of Llama 3.1 scaling, at base 500000, dim 128: 44 pairs of the
+    mid band with blend weights spread over (0, 1)."""
+    dim, base = 128, 500000.0
+    factor, low, high, ctx = LLAMA31
+    got, amp = orc.rope_frequencies(orc.rope_params(
+        dim, 1, base=base, banded_factor=factor, low_freq_factor=low, high_freq_factor=high,
+        original_context_length=ctx))
+    want = rope_freqs64(dim, base, banded=LLAMA31)
+    plain = rope_freqs64(dim, base)
+    wl = 2 * math.pi / plain
+    mid = (wl >= ctx / high) & (wl <= ctx / low)
+    # No wavelength sits within 1e-4 of a band edge (where f32 and f64 could
+    # classify a pair differently), and every band is populated.
+    for edge in (ctx / high, ctx / low):
+        assert np.min(np.abs(wl / edge - 1.0)) > 1e-4
+    smooth = (ctx / wl[mid] - low) / (high - low)
+    assert (wl < ctx / high).sum() >= 10 and (wl > ctx / low).sum() >= 10 and mid.sum() >= 3
+    assert np.any(np.abs(smooth - 0.5) > 0.2)
+    assert max_rel_err(got, want) <= 2e-6
+    assert np.all(amp == 1.0)
+    # The check has teeth: a swapped blend misses by far more than the bar.
+    assert max_rel_err(got, rope_freqs64(dim, base, banded=LLAMA31, mutant="swapped_blend")) > 1e-2
+
+
+@pytest.mark.parametrize("low,high", [(2.5, 20.0), (3.0, 11.0), (7.0, 7.0)])
+def test_rope_yarn_ramp_against_float64(orc, low, high):
+    """YaRN's linear ramp, including its interior and the low == high nudge."""
+    dim, base, factor = 64, 10000.0, 4.0
+    got, amp = orc.rope_frequencies(orc.rope_params(dim, 1, base=base, yarn_factor=factor,
+                                                    yarn_low=low, yarn_high=high))
+    want = rope_freqs64(dim, base, yarn=(factor, low, high))
+    assert max_rel_err(got, want) <= 2e-6
+    interior = (np.arange(dim // 2) > low) & (np.arange(dim // 2) < high)
+    if low != high:
+        assert interior.sum() >= 7
+        assert max_rel_err(got, rope_freqs64(dim, base, yarn=(factor, low, high),
+                                             mutant="swapped_ramp")) > 1e-2
+
+
+@pytest.mark.parametrize("form", [
+    dict(scale=0.25),
+    dict(scale=3.0),
+    dict(amplitude=1.25),
+    dict(scale=3.0, amplitude=0.8, banded=LLAMA31, base=500000.0),
+    dict(scale=0.25, amplitude=1.25, yarn=(4.0, 2.5, 20.0)),
+    dict(amplitude=1.25, yarn=(4.0, 2.5, 20.0), rotated=20),
+    dict(scale=3.0, banded=LLAMA31, base=500000.0, half_split=1),
+])
+def test_rope_scaled_positions_and_amplitude_against_float64(orc, form):
+    """The rotation with position `scale`, `amplitude` and the scaled
+    frequencies, against the float64 statement (bar: 1e-4 of each pair's norm;
+    the f32 angle position * f carries ~1e-7 of the angle, up to ~100 rad here).
+    Each planted mistake -- positions divided by the scale, the amplitude
+    dropped, the blend or ramp swapped -- misses by at least 1e-2."""
+    dim, heads, rows, offset = 64, 2, 9, 23
+    kw = dict(form)
+    scale = kw.pop("scale", 1.0)
+    amplitude = kw.pop("amplitude", 1.0)
+    half_split = kw.pop("half_split", 0)
+    base = kw.pop("base", 10000.0)
+    params = dict(base=base, scale=scale, amplitude=amplitude, position_offset=offset,
+                  half_split=half_split)
+    if "banded" in kw:
+        f, lo, hi, c = kw["banded"]
+        params.update(banded_factor=f, low_freq_factor=lo, high_freq_factor=hi,
+                      original_context_length=c)
+        # Scale the context down so that these 64-wide heads reach every band.
+        kw["banded"] = (f, lo, hi, 256.0)
+        params["original_context_length"] = 256.0
+    if "yarn" in kw:
+        f, lo, hi = kw["yarn"]
+        params.update(yarn_factor=f, yarn_low=lo, yarn_high=hi)
+    if "rotated" in kw:
+        params["rotated_pairs"] = kw["rotated"]
+    x = orc.hashed_values(rows * heads * (dim + 8), 40).reshape(rows, heads * (dim + 8))
+    got, st = orc.rope(x, orc.rope_params(dim, heads, **params))
+    assert st == 0
+    want = rope_full64(x, dim, heads, offset, scale, amplitude, half_split, base=base, **kw)
+    assert pair_err(got, want, dim, heads, half_split) <= 1e-4
+    # Columns past `dimension` in each head pass through.
+    hw = dim + 8
+    for h in range(heads):
+        assert_bitexact(got[:, h * hw + dim:(h + 1) * hw], x[:, h * hw + dim:(h + 1) * hw])
+    mutants = []
+    if scale != 1.0:
+        mutants.append("divided_scale")
+    if amplitude != 1.0:
+        mutants.append("dropped_amplitude")
+    if "banded" in kw:
+        mutants.append("swapped_blend")
+    if "yarn" in kw:
+        mutants.append("swapped_ramp")
+    for m in mutants:
+        bad = rope_full64(x, dim, heads, offset, scale, amplitude, half_split, mutant=m,
+                          base=base, **kw)
+        assert pair_err(got, bad, dim, heads, half_split) > 1e-2, m
+
+
 # ---- matmul ------------------------------------------------------------------------------
+
+def test_threaded_oracle_helpers_equal_the_single_threaded_oracle(orc):
+    """tests/reference_chain.py splits products by rows and attention by heads
+    over host threads; every value must be the single-threaded oracle's."""
+    from reference_chain import attention, matmul
+    a = orc.uniform(300 * 257, 1, -1.0, 1.0).reshape(300, 257)
+    b = orc.uniform(257 * 190, 2, -1.0, 1.0).reshape(257, 190)
+    r = orc.uniform(300 * 190, 3, -1.0, 1.0).reshape(300, 190)
+    for addend, mode in ((None, 0), (r, 2)):
+        want, st = orc.matmul(a, b, addend=addend, addend_mode=mode)
+        assert st == 0
+        got = matmul(orc, a, b, addend=addend, threads=7)
+        assert_bitexact(got, want, f"threaded matmul (addend mode {mode})")
+    seq, kv, H, Hkv, d = 40, 64, 6, 2, 16
+    q = orc.normal(seq * H * d, 4).reshape(seq, H * d)
+    k = orc.normal(kv * Hkv * d, 5).reshape(kv, Hkv * d)
+    v = orc.normal(kv * Hkv * d, 6).reshape(kv, Hkv * d)
+    p = orc.attention_params(seq, kv, H, d, kv_head_count=Hkv, causal=True, key_count=50)
+    want, st = orc.attention(q, k, v, p)
+    assert st == 0
+    assert_bitexact(attention(orc, q, k, v, p, threads=4), want, "threaded attention")
+
 
 def test_matmul_golden_and_exact(orc, fx):
     e = fx["matmul"]
