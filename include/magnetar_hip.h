@@ -218,6 +218,22 @@ typedef struct {
 mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k, const float* v,
                                float* out, const mhip_attention_params* params);
 
+/* Allocation-free matmul. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, paths and results
+ * as mhip_matmul_f32 (bit for bit), but the split-k / stream-K / GEMV partial
+ * sums go to a fixed device array of MHIP_NOALLOC_SCRATCH_BYTES that the
+ * library holds on each GPU it runs on until the process ends, instead of
+ * the context's grow-only workspace; it calls no hipMalloc or hipFree. A
+ * product whose partial sums need more returns MHIP_SHAPE_UNSUPPORTED (the
+ * detail names the bytes needed). Every context on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (different streams or
+ * contexts) race; calls ordered on one stream do not. */
+#define MHIP_NOALLOC_SCRATCH_BYTES (128ull << 20)
+mhip_status mhip_matmul_f32_noalloc(mhip_ctx* ctx, const float* a, const float* b, float* out,
+                                    uint64_t m, uint64_t k, uint64_t n, int transpose_a,
+                                    int transpose_b, const float* addend, int addend_mode);
+
 /* Compact bf16 weights (execute-native-half-precision, src/kernels.rs:1665-1723):
  * the matmul with b given as bf16 bit patterns ([k, n], or [n, k] when
  * transpose_b) and the embedding lookup with a bf16 table. Each widens the

@@ -34,6 +34,11 @@ struct mhip_ctx {
     // Grow-only device workspace for split-k partial sums (matmul, attention).
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    // Set only for the duration of an mhip_matmul_f32_noalloc call: the
+    // device's fixed scratch array, which the matmul then uses instead of the
+    // workspace (never grown; a larger need is refused).
+    void* fixed_scratch = nullptr;
+    size_t fixed_scratch_bytes = 0;
 
     // Step capture: while `capturing`, launches on the stream are recorded
     // into a HIP graph instead of running. Launches whose attribute is in
@@ -166,6 +171,11 @@ const uint64_t* advance_ptr(mhip_ctx* ctx, uint32_t bit, uint64_t max_offset);
 // attention chunk records). Growing it waits for the stream; a buffer a live
 // graph may read is retired, not freed. Refused while capturing.
 mhip_status workspace(mhip_ctx* ctx, size_t bytes, void** out);
+
+// Looks up (once per device, with the context's device current) the device
+// address of the allocation-free matmul's fixed scratch array; called when a
+// context is created. Returns it through `out` when not null.
+mhip_status noalloc_scratch(mhip_ctx* ctx, float** out);
 
 // The device (frequency, amplitude) table of a RoPE call's pairs, computed
 // on the host with the f32 operations of src/kernels.cu:1197-1221 and cached

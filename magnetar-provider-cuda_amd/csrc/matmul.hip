@@ -38,6 +38,8 @@
 #include <type_traits>
 
 #include "common.hpp"
+
+#include <mutex>
 #include "internal.hpp"
 
 namespace {
@@ -50,8 +52,19 @@ constexpr int kGemvMaxRows = 8;
 constexpr uint64_t kGemvSmallProduct = 1ull << 26;
 
 // Split-k partial sums live in the context's workspace; stream order makes
-// reuse by the next call safe.
+// reuse by the next call safe. During mhip_matmul_f32_noalloc they live in
+// the device's fixed scratch array instead, and a product that needs more
+// than it holds is refused.
 mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
+    if (ctx->fixed_scratch) {
+        if (bytes > ctx->fixed_scratch_bytes)
+            return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
+                              "matmul: this product needs " + std::to_string(bytes) +
+                                  " bytes of scratch; the allocation-free matmul has " +
+                                  std::to_string(ctx->fixed_scratch_bytes));
+        *out = static_cast<float*>(ctx->fixed_scratch);
+        return MHIP_OK;
+    }
     void* p = nullptr;
     mhip_status st = mhip::workspace(ctx, bytes, &p);
     *out = static_cast<float*>(p);
@@ -1224,6 +1237,72 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
 extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
                                        uint64_t m, uint64_t k, uint64_t n, int transpose_a,
                                        int transpose_b, const float* addend, int addend_mode) {
+    return matmul_impl<float>(ctx, a, b, out, m, k, n, transpose_a, transpose_b, addend, addend_mode);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free matmul: the partial sums in a fixed device array
+// ---------------------------------------------------------------------------
+
+// The scratch of mhip_matmul_f32_noalloc (split-k, stream-K and GEMV partial
+// sums). Each GPU the library runs on holds its own copy until the process
+// ends. On the host this name is a stand-in, not a device address: host code
+// only ever uses the address hipGetSymbolAddress gives for a device.
+static __device__ __align__(256) float scratch[MHIP_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mutex;
+float* scratch_address[kScratchDevices] = {};
+
+}  // namespace
+
+// The device address of `scratch` on the context's device: looked up once
+// per device, with that device current, when the first context on it is
+// created (or, if that failed, on the entry point's next call there).
+mhip_status mhip::noalloc_scratch(mhip_ctx* ctx, float** out) {
+    if (ctx->device < 0 || ctx->device >= kScratchDevices)
+        return mhip::fail(MHIP_DEVICE_UNAVAILABLE, "allocation-free matmul: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    float*& address = scratch_address[ctx->device];
+    if (!address) {
+        hipError_t err = hipSetDevice(ctx->device);
+        void* p = nullptr;
+        if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return mhip::from_hip(err, "locating the allocation-free matmul's scratch");
+        address = static_cast<float*>(p);
+    }
+    if (out) *out = address;
+    return MHIP_OK;
+}
+
+namespace {
+
+// Points the context's matmul scratch at the fixed array for one call.
+struct FixedScratch {
+    mhip_ctx* ctx;
+    FixedScratch(mhip_ctx* c, float* p) : ctx(c) {
+        ctx->fixed_scratch = p;
+        ctx->fixed_scratch_bytes = MHIP_NOALLOC_SCRATCH_BYTES;
+    }
+    ~FixedScratch() {
+        ctx->fixed_scratch = nullptr;
+        ctx->fixed_scratch_bytes = 0;
+    }
+};
+
+}  // namespace
+
+extern "C" mhip_status mhip_matmul_f32_noalloc(mhip_ctx* ctx, const float* a, const float* b,
+                                               float* out, uint64_t m, uint64_t k, uint64_t n,
+                                               int transpose_a, int transpose_b,
+                                               const float* addend, int addend_mode) {
+    MHIP_REQUIRE_CTX(ctx);
+    float* p = nullptr;
+    mhip_status st = mhip::noalloc_scratch(ctx, &p);
+    if (st != MHIP_OK) return st;
+    FixedScratch use(ctx, p);
     return matmul_impl<float>(ctx, a, b, out, m, k, n, transpose_a, transpose_b, addend, addend_mode);
 }
 

@@ -172,6 +172,9 @@ mhip_status mhip_ctx_create(int ordinal, mhip_ctx** out) {
         mhip_ctx_destroy(ctx);
         return st;
     }
+    // The allocation-free matmul's scratch address on this device (a failure
+    // here is reported by that entry point's own call).
+    (void)mhip::noalloc_scratch(ctx, nullptr);
     *out = ctx;
     return MHIP_OK;
 }

@@ -137,6 +137,7 @@ SIGNATURES = {
     "mhip_rope_params_default": [ctypes.POINTER(RopeParams), _U64, _U64],
     "mhip_rope_f32": [_CTX, _P, _P, _U64, _U64, ctypes.POINTER(RopeParams)],
     "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
+    "mhip_matmul_f32_noalloc": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
     "mhip_attention_f32": [_CTX, _P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
     "mhip_kv_write_f32": [_CTX, _P, _U64, _U64, _P, _U64, _U64],
     "mhip_matmul_bf16w_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, ctypes.c_int, ctypes.c_int, _P,
