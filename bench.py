@@ -7,7 +7,9 @@ hot-path Kernel at its BASELINE shape (`kernels`), each as algorithmic
 GB/s or TFLOP/s over the average launch time from HIP events recorded on
 the library's own stream, and as a fraction of the MI355X roofline.
 Inputs are resident in HBM before timing starts. The CPU oracle is timed on
-a bounded sample of the headline workload on this host (`cpu_baseline`).
+a bounded sample of the headline workload on this host (`cpu_baseline`), and
+beside every other kernel on a bounded sample of its workload
+(`kernels.<name>.cpu`).
 """
 from __future__ import annotations
 
@@ -251,7 +253,7 @@ def selection_cases(dev, orc):
     return cases
 
 
-def decoder_cases(dev, orc):
+def decoder_cases(dev, orc, graphs=True):
     """The chained decoder block: config 0 (tiny, seq 32) and config 4
     (Llama-2-7B shapes: prefill 512, decode one token at KV 2048)."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
@@ -275,12 +277,13 @@ def decoder_cases(dev, orc):
     cases.append(Case("decoder_c1_seq32", lambda i: b0.forward(ids0, 0, out0), w0, "hbm",
                       [32, 256], tokens=32))
     # The same block captured once as a HIP graph and replayed (launch-bound).
-    b0.forward(ids0, 0, out0)
-    dev.capture_begin(0)
-    b0.forward(ids0, 0, out0)
-    g0 = dev.capture_end()
-    cases.append(Case("decoder_c1_seq32_graph", lambda i: g0.launch(0), w0, "hbm", [32, 256],
-                      tokens=32))
+    if graphs:
+        b0.forward(ids0, 0, out0)
+        dev.capture_begin(0)
+        b0.forward(ids0, 0, out0)
+        g0 = dev.capture_end()
+        cases.append(Case("decoder_c1_seq32_graph", lambda i: g0.launch(0), w0, "hbm", [32, 256],
+                          tokens=32))
     big = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     b4 = block(big, 4, 2049, 512)
     ids_p = dev.upload(orc.token_ids(512, seed(4, 8), 32000))
@@ -297,12 +300,13 @@ def decoder_cases(dev, orc):
     # A decode step captured with position, cache row and key count advancing
     # (here at the last cache row, so replays run at offset 0).
     from magnetar_hip.device import ADVANCE_KEY_COUNT, ADVANCE_POSITION_OFFSET, ADVANCE_ROW_OFFSET
-    b4.forward(ids_d, 2048, out_d)
-    dev.capture_begin(ADVANCE_POSITION_OFFSET | ADVANCE_KEY_COUNT | ADVANCE_ROW_OFFSET)
-    b4.forward(ids_d, 2048, out_d)
-    g4 = dev.capture_end()
-    cases.append(Case("decoder_c5_decode_kv2048_graph", lambda i: g4.launch(0),
-                      weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
+    if graphs:
+        b4.forward(ids_d, 2048, out_d)
+        dev.capture_begin(ADVANCE_POSITION_OFFSET | ADVANCE_KEY_COUNT | ADVANCE_ROW_OFFSET)
+        b4.forward(ids_d, 2048, out_d)
+        g4 = dev.capture_end()
+        cases.append(Case("decoder_c5_decode_kv2048_graph", lambda i: g4.launch(0),
+                          weight_bytes + kv_bytes, "hbm", [1, 4096], tokens=1))
     # Config 4 decode with compact bf16 weights (a bf16 checkpoint): half the
     # weight bytes, the same f32 arithmetic.
     b4h = block(big, 4, 2049, 1, bf16=True)
@@ -375,6 +379,186 @@ def cpu_baseline(orc, runs=5, run_s=1.5):
             "cpu_model": _cpu_model(), "nproc": os.cpu_count()}
 
 
+# ---------------------------------------------------------------------------
+# Per-kernel CPU legs: the oracle (oracle/oracle.c, the reference CPU
+# Provider's arithmetic) timed beside every kernel on a bounded sample of the
+# same workload, on this host. Reported baselines only.
+# ---------------------------------------------------------------------------
+
+class CpuLeg:
+    """`run(r0, r1)` does units [r0, r1) of a case's workload on the oracle
+    (rows, heads, rows of a product, whole block calls); `units` is the
+    workload's count and `data_units` how many the host sample holds; `work`
+    is the GPU case's algorithmic bytes or flops per unit and `tokens` its
+    tokens per unit. `split`: units are divided over host threads; otherwise
+    one call runs them (`cores` then says how many threads that call uses)."""
+
+    def __init__(self, run, units, work, what, data_units=None, tokens=0.0, split=True, cores=1):
+        self.run, self.units, self.work, self.what = run, units, work, what
+        self.data_units = data_units or units
+        self.tokens, self.split, self.cores = tokens, split, cores
+
+
+def time_cpu_leg(leg, bound, threads, target_s=0.4, runs=3):
+    from concurrent.futures import ThreadPoolExecutor
+    t = time.perf_counter()
+    leg.run(0, 1)  # warm-up, and the time of one unit
+    per_unit = time.perf_counter() - t
+    n = min(threads, leg.data_units) if leg.split else 1
+    # Split legs cover at most the host sample; a single-call leg repeats
+    # its call up to the time target.
+    cap = leg.data_units if leg.split else 100000
+    units = int(min(cap, max(n, target_s * n / max(per_unit, 1e-7))))
+    bounds = np.linspace(0, units, n + 1).astype(int)
+    with ThreadPoolExecutor(n) as pool:
+        def once():
+            if n == 1:
+                leg.run(0, units)
+            else:
+                list(pool.map(lambda i: leg.run(int(bounds[i]), int(bounds[i + 1])), range(n)))
+        once()
+        times = []
+        for _ in range(runs):
+            t = time.perf_counter()
+            once()
+            times.append(time.perf_counter() - t)
+    sec = float(np.median(times))
+    rate = leg.work * units / sec
+    out = {"value": round(rate / (1e9 if bound == "hbm" else 1e12), 6),
+           "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+           "cores": n if leg.split else leg.cores, "kind": "port",
+           "sample": (f"{units} of {leg.units} {leg.what}" if leg.split else f"{units} {leg.what}")
+                     + f", median of {runs} runs ({sec * 1e3:.1f} ms each) after a warm-up"}
+    if leg.tokens:
+        out["tokens_per_s"] = round(leg.tokens * units / sec, 2)
+    return out
+
+
+def cpu_legs(orc, names):
+    """CpuLeg per bench case name (only those in `names`). Inputs are host
+    samples of each case's shape; their values (numpy's generator, same
+    distributions) do not change the oracle's time."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from reference_chain import host_threads, reference_block
+    from magnetar_hip.decoder import Shapes
+    rng = np.random.default_rng(7)
+    normal = lambda shape, std=1.0, mean=0.0: (rng.standard_normal(shape, np.float32) * std + mean)
+    legs = {}
+    want = lambda *ns: any(n in names for n in ns)
+    rows, cols = 8192, 4096
+    row_bytes = cols * 4
+    if want("add", "mul", "residual_add", "silu", "silu_mul", "rmsnorm", "softmax", "rope"):
+        x, y = normal((rows, cols)), normal((rows, cols))
+        sm = x * np.float32(2.0)
+        gain = normal(cols, 0.1, 1.0)
+        what = "rows of [8192, 4096]"
+        legs["add"] = CpuLeg(lambda a, b: orc.add(x[a:b], y[a:b]), rows, 3 * row_bytes, what)
+        legs["mul"] = CpuLeg(lambda a, b: orc.mul(x[a:b], y[a:b]), rows, 3 * row_bytes, what)
+        legs["residual_add"] = legs["add"]
+        legs["silu"] = CpuLeg(lambda a, b: orc.silu(x[a:b]), rows, 2 * row_bytes, what)
+        legs["silu_mul"] = CpuLeg(lambda a, b: orc.silu_mul(x[a:b], y[a:b]), rows, 3 * row_bytes, what)
+        legs["rmsnorm"] = CpuLeg(lambda a, b: orc.rmsnorm(x[a:b], gain, 1e-5), rows,
+                                 2 * row_bytes, what)
+        legs["softmax"] = CpuLeg(lambda a, b: orc.softmax_rows(sm[a:b]), rows, 2 * row_bytes, what)
+        legs["rope"] = CpuLeg(lambda a, b: orc.rope(x[a:b], orc.rope_params(128, 32, position_offset=a)),
+                              rows, 2 * row_bytes, what)
+    if want("embedding"):
+        vocab = 16384  # a 268 MB slice of the 128000-row table: gathers stay DRAM reads
+        table = normal((vocab, cols))
+        ids = rng.integers(0, vocab, 8192).astype(np.float32)
+        legs["embedding"] = CpuLeg(lambda a, b: orc.embedding(table, ids[a:b]), 8192,
+                                   2 * row_bytes + 4, "ids into a [16384, 4096] table")
+    for dname, dt in (("f16", 0), ("bf16", 1)):
+        if want(f"add_{dname}", f"mul_{dname}"):
+            ha = orc.encode_half(normal((4096, 4096)), dt)
+            hb = orc.encode_half(normal((4096, 4096)), dt)
+            for op in ("add", "mul"):
+                legs[f"{op}_{dname}"] = CpuLeg(
+                    (lambda a, b, ha=ha, hb=hb, op=op, dt=dt: orc.half_binary(ha[a:b], hb[a:b], dt, op)),
+                    16384, 3 * 4096 * 2, "rows of 4096 of the 64M-element tensors", data_units=4096)
+    for size in (1024, 2048, 4096, 8192):
+        if want(f"matmul_{size}"):
+            a_m, b_m = normal((size, size)), normal((size, size))
+            legs[f"matmul_{size}"] = CpuLeg(
+                (lambda r0, r1, a_m=a_m, b_m=b_m: orc.matmul_rows(a_m, b_m, r0, r1)), size,
+                2.0 * size * size, f"rows of the {size}^3 product")
+    if want("matmul_1x4096x11008", "matmul_1x4096x11008_bf16w"):
+        a1, b1 = normal((1, 4096)), normal((4096, 11008))
+        gemv = lambda r0, r1: [orc.matmul_rows(a1, b1, 0, 1) for _ in range(r0, r1)]
+        legs["matmul_1x4096x11008"] = CpuLeg(gemv, 1, 4 * (4096 * 11008 + 4096 + 11008),
+                                             "whole products in a row", split=False)
+        legs["matmul_1x4096x11008_bf16w"] = CpuLeg(gemv, 1, 2 * 4096 * 11008 + 4 * (4096 + 11008),
+                                                   "whole products in a row (over the widened f32 "
+                                                   "weight)", split=False)
+    if want("attention_prefill"):
+        S, H, d = 2048, 32, 128
+        q, k, v = normal((S, H * d)), normal((S, H * d)), normal((S, H * d))
+        ap = orc.attention_params(S, S, H, d, causal=True)
+        legs["attention_prefill"] = CpuLeg(lambda a, b: orc.attention(q, k, v, ap, heads=(a, b)),
+                                           4 * H, 4.0 * d * S * (S + 1) / 2,
+                                           "(batch, head) pairs of B4 H32 S2048 d128", data_units=H)
+    if want("attention_decode"):
+        KV, H, d = 4096, 32, 128
+        q, k, v = normal((1, H * d)), normal((KV, H * d)), normal((KV, H * d))
+        ad = orc.attention_params(1, KV, H, d, causal=True)
+        legs["attention_decode"] = CpuLeg(lambda a, b: orc.attention(q, k, v, ad, heads=(a, b)),
+                                          8 * H, 2 * KV * d * 4 + 2 * d * 4,
+                                          "(batch, head) pairs of B8 H32 KV4096 d128", data_units=H)
+    if want("greedy_select_32000"):
+        logits = normal(32000)
+        legs["greedy_select_32000"] = CpuLeg(
+            lambda a, b: [orc.greedy_select(logits) for _ in range(a, b)], 1, 32000 * 4,
+            "selections over a 32000-column row", split=False)
+    if want("kv_write_1x4096"):
+        store, row = np.zeros((2048, 4096), np.float32), normal(4096)
+
+        def kv(a, b):
+            for r in range(a, b):
+                store[r % 2048] = row
+        legs["kv_write_1x4096"] = CpuLeg(kv, 2048, 2 * 4096 * 4,
+                                         "row appends into a [2048, 4096] store (numpy copy)",
+                                         split=False)
+    if want("decoder_c1_seq32", "decoder_c1_seq32_graph"):
+        tiny = Shapes(vocab=1024, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=688)
+        wt = {n: (np.ones(sh, np.float32) if n.endswith("norm") else normal(sh, 0.02))
+              for n, sh in tiny.weight_shapes().items()}
+        ids0 = rng.integers(0, 1024, 32).astype(np.float32)
+        z = np.zeros((32, 256), np.float32)
+        run = lambda a, b: [reference_block(orc, tiny, wt, ids0, 0, z, z, threads=1) for _ in range(a, b)]
+        leg = CpuLeg(run, 1, 4 * (4 * 256 * 256 + 3 * 256 * 688), "block calls of 32 tokens",
+                     tokens=32, split=False)
+        legs["decoder_c1_seq32"] = legs["decoder_c1_seq32_graph"] = leg
+    big_names = ("decoder_c5_prefill512", "decoder_c5_decode_kv2048",
+                 "decoder_c5_decode_kv2048_graph", "decoder_c5_decode_kv2048_bf16w")
+    if want(*big_names):
+        big = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
+        wb = {n: (np.ones(sh, np.float32) if n.endswith("norm") else normal(sh, 0.02))
+              for n, sh in big.weight_shapes().items()}
+        threads = host_threads()
+        if want("decoder_c5_prefill512"):
+            seq = 64
+            ids_p = rng.integers(0, 32000, seq).astype(np.float32)
+            zp = np.zeros((seq, 4096), np.float32)
+            flops = 2.0 * seq * (4 * 4096 * 4096 + 3 * 4096 * 11008) + 4.0 * 128 * seq * (seq + 1) / 2 * 32
+            legs["decoder_c5_prefill512"] = CpuLeg(
+                lambda a, b: [reference_block(orc, big, wb, ids_p, 0, zp, zp, threads=threads)
+                              for _ in range(a, b)],
+                1, flops, "block calls of a 64-token prefill (the 512-token call's products "
+                          "split by rows over threads)", tokens=seq, split=False, cores=threads)
+        kc, vc = normal((2049, 4096), 0.5), normal((2049, 4096), 0.5)
+        ids_d = rng.integers(0, 32000, 1).astype(np.float32)
+        weight_bytes = 4 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
+        dec = CpuLeg(lambda a, b: [reference_block(orc, big, wb, ids_d, 2048, kc, vc, threads=1)
+                                   for _ in range(a, b)],
+                     1, weight_bytes + 2 * 2049 * 4096 * 4, "decode steps at KV 2048", tokens=1,
+                     split=False)
+        legs["decoder_c5_decode_kv2048"] = legs["decoder_c5_decode_kv2048_graph"] = dec
+        legs["decoder_c5_decode_kv2048_bf16w"] = CpuLeg(
+            dec.run, 1, weight_bytes // 2 + 2 * 2049 * 4096 * 4,
+            "decode steps at KV 2048 (over the widened f32 weights)", tokens=1, split=False)
+    return {n: leg for n, leg in legs.items() if n in names}
+
+
 def _reshape(arr, shape):
     from magnetar_hip.device import DeviceArray
     return DeviceArray(arr.device, arr.ptr, shape, arr.dtype, arr.half, owned=False)
@@ -400,7 +584,8 @@ def main(argv=None):
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--only", default="", help="comma-separated kernel names")
-    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--exclude", default="", help="comma-separated kernel names to skip")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     parser.add_argument("--preheat", type=float, default=PREHEAT_S,
                         help="untimed seconds of GPU time each case runs first (clock ramp)")
     args = parser.parse_args(argv)
@@ -414,6 +599,7 @@ def main(argv=None):
     dev = magnetar_hip.Device(0)
     info = dev.info()
     only = set(filter(None, args.only.split(",")))
+    exclude = set(filter(None, args.exclude.split(",")))
     wanted = lambda prefix: not only or any(name.startswith(prefix) for name in only)
     cases = []
     if wanted("matmul"):
@@ -426,12 +612,13 @@ def main(argv=None):
     if wanted("greedy") or wanted("kv_write"):
         cases += selection_cases(dev, orc)
     if wanted("decoder"):
-        cases += decoder_cases(dev, orc)
+        graphs = not {"decoder_c1_seq32_graph", "decoder_c5_decode_kv2048_graph"} <= exclude
+        cases += decoder_cases(dev, orc, graphs)
     if any(name.startswith("calibration") for name in only):
         cases += calibration_cases(dev, orc)
     results = {}
     for case in cases:
-        if only and case.name not in only:
+        if (only and case.name not in only) or case.name in exclude:
             continue
         results[case.name] = case.measure(dev, args.steps, args.warmup, args.preheat)
         r = results[case.name]
@@ -446,7 +633,17 @@ def main(argv=None):
         roofline = {"bound": "mfma", "achieved": round(head["achieved"], 2),
                     "peak": head["peak"], "unit": head["unit"],
                     "frac": round(head["frac"], 4), "traffic": TRAFFIC.get(HEADLINE)}
-    base = None if args.no_cpu else cpu_baseline(orc)
+    base = None if args.no_cpu or HEADLINE not in results else cpu_baseline(orc)
+    if not args.no_cpu:
+        threads = _host_threads()
+        legs = cpu_legs(orc, set(results))
+        for name, leg in legs.items():
+            r = results[name]
+            r["cpu"] = time_cpu_leg(leg, r["bound"], threads)
+            c = r["cpu"]
+            print(f"# cpu {name:14s} {c['value']:10.4f} {c['unit']} on {c['cores']} threads"
+                  + (f"  {c['tokens_per_s']:.2f} tokens/s" if "tokens_per_s" in c else ""),
+                  file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": round(head["achieved"], 2) if head else None,
@@ -470,8 +667,11 @@ def main(argv=None):
         "kernels": {k: dict({"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),
                              "unit": v["unit"], "frac": round(v["frac"], 4), "shape": v["shape"]},
                             **({"tokens_per_s": round(v["tokens_per_s"], 1)}
-                               if "tokens_per_s" in v else {}))
+                               if "tokens_per_s" in v else {}),
+                            **({"cpu": v["cpu"]} if "cpu" in v else {}))
                     for k, v in results.items()},
+        "cpu_host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count(),
+                     "threads": _host_threads()},
     }
     print(json.dumps(line))
     dev.close()

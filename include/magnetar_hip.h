@@ -288,8 +288,9 @@ mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offs
 mhip_status mhip_capture_abort(mhip_ctx* ctx);
 int mhip_capture_active(const mhip_ctx* ctx);
 /* Runs the step with every advancing attribute increased by `offset`
- * (ShapeUnsupported beyond the bound). The failure flags are cleared at the
- * start of every run. */
+ * (ShapeUnsupported beyond the bound). Its launches set failure flags as
+ * eager calls do: a flag stays set, whichever call or replay set it, until
+ * mhip_check_flags reads and clears it. */
 mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset);
 uint64_t mhip_graph_max_offset(const mhip_graph* graph);
 mhip_status mhip_graph_destroy(mhip_graph* graph);

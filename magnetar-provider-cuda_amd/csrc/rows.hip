@@ -110,12 +110,59 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
     }
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Softmax partial state over a set of entries: their maximum m (NaN-ignoring,
+// as fmaxf) and s = the sum of exp(x - m) over them. Two states merge into
+// the state of their union by rescaling each sum to the larger maximum; no
+// finite maximum leaves s = 0 (the row then fails). A NaN entry makes s NaN,
+// which every merge keeps, so the whole row comes out NaN as in the
+// reference's sum.
+__device__ __forceinline__ void merge_state(float& m, float& s, float m2, float s2) {
+    const float mm = fmaxf(m, m2);
+    if (mm == -INFINITY) {
+        m = mm;
+        s = 0.0f;
+        return;
+    }
+    s = s * exp2f((m - mm) * kLog2e) + s2 * exp2f((m2 - mm) * kLog2e);
+    m = mm;
+}
+
+// Merges the states of the G threads of this row's group; every thread gets
+// the same (m, s). The butterfly merges both partners in the same order up
+// to commutation, so all lanes agree bit for bit; for G == 256 the four waves'
+// states meet in `scratch` and every thread merges them in wave order.
+template <int G>
+__device__ __forceinline__ void group_merge(float& m, float& s, float2* scratch) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64);
+        const float s2 = __shfl_xor(s, off, 64);
+        merge_state(m, s, m2, s2);
+    }
+    if constexpr (G == 256) {
+        const int wave = threadIdx.x / 64;
+        if ((threadIdx.x & 63) == 0) scratch[wave] = make_float2(m, s);
+        __syncthreads();
+        m = scratch[0].x;
+        s = scratch[0].y;
+#pragma unroll
+        for (int w = 1; w < 4; ++w) merge_state(m, s, scratch[w].x, scratch[w].y);
+    }
+}
+
+// One pass over the row in registers: each thread takes the maximum m_t of
+// its own entries and e = exp(x - m_t) for each of them (exp2 of the
+// difference scaled by log2 e), then the group merges the (max, sum) states
+// once, and the output is e * exp(m_t - M) / S, the reciprocal of S taken
+// once per thread. Within a few ulp of exp(x - M) / S.
 template <int G, int VPT>
 __global__ __launch_bounds__(kThreads) void softmax_vec_kernel(const float* __restrict__ in,
                                                                float* __restrict__ out,
                                                                uint64_t rows, uint64_t cols,
                                                                uint32_t* flags) {
-    __shared__ float scratch[4];
+    __shared__ float2 scratch[4];
     constexpr int kRowsPerBlock = kThreads / G;
     const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
     const int lane = threadIdx.x % G;
@@ -123,35 +170,40 @@ __global__ __launch_bounds__(kThreads) void softmax_vec_kernel(const float* __re
     const bool live = row < rows;
     const float4* x4 = reinterpret_cast<const float4*>(in) + row * cols4;
     float4 x[VPT];
-    float m = -INFINITY;
+    float mt = -INFINITY;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
         x[v] = (live && c < cols4) ? mhip::load_nt(x4 + c)
                                    : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        m = fmaxf(m, fmaxf(fmaxf(x[v].x, x[v].y), fmaxf(x[v].z, x[v].w)));
+        mt = fmaxf(mt, fmaxf(fmaxf(x[v].x, x[v].y), fmaxf(x[v].z, x[v].w)));
     }
-    m = group_reduce<G>(m, MaxOp{}, scratch);
-    // A row with no finite maximum fails the call (src/kernels.rs:4371-4378).
-    const bool bad = !isfinite(m);
-    if (live && bad && lane == 0) atomicOr(flags, MHIP_FLAG_SOFTMAX_NON_FINITE);
-    float s = 0.0f;
+    // Entries of a thread whose own maximum is -inf are all -inf (or NaN):
+    // their exponentials are taken against 0 (giving 0, or NaN).
+    const float base = mt == -INFINITY ? 0.0f : mt;
+    float st = 0.0f;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
-        uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        if (c < cols4 && !bad) {
-            x[v] = make_float4(expf(x[v].x - m), expf(x[v].y - m), expf(x[v].z - m),
-                               expf(x[v].w - m));
-            s += (x[v].x + x[v].y) + (x[v].z + x[v].w);
-        }
+        x[v] = make_float4(exp2f((x[v].x - base) * kLog2e), exp2f((x[v].y - base) * kLog2e),
+                           exp2f((x[v].z - base) * kLog2e), exp2f((x[v].w - base) * kLog2e));
+        st += (x[v].x + x[v].y) + (x[v].z + x[v].w);
     }
-    s = group_reduce<G>(s, SumOp{}, scratch);
-    if (!live || bad) return;
+    float M = mt, S = st;
+    group_merge<G>(M, S, scratch);
+    // A row with no finite maximum fails the call (src/kernels.rs:4371-4378).
+    if (!live) return;
+    if (!isfinite(M)) {
+        if (lane == 0) atomicOr(flags, MHIP_FLAG_SOFTMAX_NON_FINITE);
+        return;
+    }
+    const float scale = exp2f((mt - M) * kLog2e) * (1.0f / S);
     float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
         uint64_t c = lane + static_cast<uint64_t>(v) * G;
-        if (c < cols4) mhip::store_nt(o4 + c, make_float4(x[v].x / s, x[v].y / s, x[v].z / s, x[v].w / s));
+        if (c < cols4)
+            mhip::store_nt(o4 + c, make_float4(x[v].x * scale, x[v].y * scale, x[v].z * scale,
+                                               x[v].w * scale));
     }
 }
 

@@ -99,13 +99,11 @@ struct mhip_graph {
 
 namespace {
 
-// Ahead of every replay of a captured step: its offset word, and the failure
-// flags cleared (the step's launches then only ever set them). One launch,
-// not a graph node: the graph holds the step's own work only.
-__global__ void replay_prologue_kernel(uint64_t* word, uint64_t value, uint32_t* flags) {
-    if (threadIdx.x == 0) *word = value;
-    flags[threadIdx.x] = 0u;
-}
+// Ahead of every replay of a captured step: its offset word. One launch, not
+// a graph node (no memset node either): the graph holds the step's own work
+// only. The failure flags are left alone: like eager calls, a replay only
+// sets them, and mhip_check_flags clears them when it reports them.
+__global__ void replay_offset_kernel(uint64_t* word, uint64_t value) { *word = value; }
 
 }  // namespace
 
@@ -430,10 +428,8 @@ mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset) {
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
                           "offset " + std::to_string(offset) + " leaves the captured bounds (at most " +
                               std::to_string(graph->max_offset) + ")");
-    // The offset is written, and the flags cleared, by a kernel on the same
-    // stream, ahead of the graph.
-    hipLaunchKernelGGL(replay_prologue_kernel, dim3(1), dim3(64), 0, ctx->stream, graph->offset,
-                       offset, ctx->flags);
+    // The offset is written by a kernel on the same stream, ahead of the graph.
+    hipLaunchKernelGGL(replay_offset_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
     mhip_status st = mhip::check_launch("writing the replay offset");
     if (st != MHIP_OK) return st;
     return mhip::from_hip(hipGraphLaunch(graph->exec, ctx->stream), "launching a captured step");

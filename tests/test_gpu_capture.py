@@ -290,6 +290,30 @@ def test_a_captured_decode_step_advances_position_cache_row_and_key_count(
     ex.release_step_capture(capture)
 
 
+def test_a_replay_keeps_a_flag_an_earlier_call_set(dev, orc):
+    """A replay sets failure flags as eager calls do and clears none: an invalid
+    embedding id recorded before a replay is still reported by the next check,
+    and the check clears it."""
+    import magnetar_hip
+    from magnetar_hip import ops
+    x = dev.upload(orc.normal(256, 5).reshape(1, 256))
+    out = dev.empty((1, 256))
+    ops.silu(dev, x, out=out)
+    dev.capture_begin(0)
+    ops.silu(dev, x, out=out)
+    graph = dev.capture_end()
+    table = dev.upload(orc.normal(32, 6).reshape(8, 4))
+    ops.embedding(dev, table, dev.upload(np.array([9.0], np.float32)))  # id past the vocab
+    graph.launch(0)
+    with pytest.raises(magnetar_hip.MagnetarHipError):
+        dev.check_flags()
+    graph.launch(0)
+    assert dev.check_flags() == 0
+    want, _ = orc.silu(orc.normal(256, 5).reshape(1, 256))
+    assert max_rel_err(out.numpy(), want) <= 1e-6
+    graph.close()
+
+
 BLOCK_CASES = [
     # hidden, heads, kv_heads, head_dim, ffn, cache rows, position, replay offsets
     (512, 8, 2, 64, 1024, 48, 20, (0, 1, 2, 3, 4)),
