@@ -4,7 +4,8 @@
 //
 // Arithmetic: decode both operands exactly to f32, one f32 add or mul, RNE
 // encode -- the reference's kernels (src/kernels.cu:2913-2939) and its exact
-// model (src/tests_conformance.rs:2334-2347). The codec matches
+// model (src/tests_conformance.rs:2334-2347); a NaN result's payload follows
+// the x86 rule of the reference CPU Provider (see nan_rule). The codec matches
 // src/half_precision.rs:14-125 bit for bit:
 //  - f16 decode uses v_cvt_f32_f16 (exact for every finite value, subnormals
 //    included) and rebuilds NaNs from their bits so a signalling payload is
@@ -71,10 +72,22 @@ __device__ __forceinline__ float materialize(float v) {
     return v;
 }
 
+// A NaN result carries a NaN operand's payload, quieted -- the second
+// operand's when both are NaN; a NaN made from non-NaN operands (inf - inf,
+// 0 * inf) is the negative default quiet NaN. That is what the reference CPU
+// Provider's compiled f32 arithmetic gives on an x86-64 host, stated
+// explicitly (the GPU's ALU would pick a NaN of its own).
+__device__ __forceinline__ float nan_rule(float x, float y, float r) {
+    if (r == r) return r;
+    const uint32_t bits = y != y ? __float_as_uint(y) | 0x00400000u
+                                 : (x != x ? __float_as_uint(x) | 0x00400000u : 0xFFC00000u);
+    return __uint_as_float(bits);
+}
+
 template <int DT, int OP>
 __device__ __forceinline__ uint32_t op1(uint32_t a, uint32_t b) {
     float x = dec<DT>(a), y = dec<DT>(b);
-    return enc<DT>(materialize(OP ? x * y : x + y));
+    return enc<DT>(nan_rule(x, y, materialize(OP ? x * y : x + y)));
 }
 
 // One 32-bit word holds two halves (low half first in memory).

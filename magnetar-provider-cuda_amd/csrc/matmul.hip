@@ -603,18 +603,34 @@ GemmPlan plan_gemm(uint64_t m, uint64_t k, uint64_t n, uint64_t bm, uint64_t bn,
 
 // Estimated seconds for an m x k x n product with one tile configuration:
 // the critical path's k slices at the configuration's measured fraction of
-// peak (shared by the workgroups a CU holds), plus the partial results'
-// traffic. Picks between the 128 x 128 and 256 x 256 kernels.
+// peak, plus the partial results' traffic. Splits are planned for
+// `plan_per_cu` workgroups per CU. The workgroups resident on a CU share its
+// MFMA pipes; below two waves per SIMD a wave's LDS reads are exposed, so
+// the fraction scales with waves per SIMD / 2 (one 4-wave workgroup per CU
+// measured about half the 2-workgroup rate). Picks among the tile kernels.
 double gemm_seconds(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n, uint64_t bm,
-                    uint64_t bn, uint64_t bk, uint64_t lds_bytes, double efficiency) {
+                    uint64_t bn, uint64_t bk, uint64_t plan_per_cu, int waves, double efficiency) {
     const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
-    const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / lds_bytes);
-    const GemmPlan p = plan_gemm(m, k, n, bm, bn, bk, per_cu * cus);
+    const uint64_t slots = plan_per_cu * cus;
+    const GemmPlan p = plan_gemm(m, k, n, bm, bn, bk, slots);
+    const uint64_t wgs = p.stream ? p.groups : p.tiles * p.splits;
+    const uint64_t resident =
+        std::max<uint64_t>(1, std::min<uint64_t>(plan_per_cu, (std::min(wgs, slots) + cus - 1) / cus));
+    const double per_simd = static_cast<double>(resident * waves) / 4.0;
+    const double occupancy = std::min(1.0, per_simd / 2.0);
     const double cu_flops = 157.3e12 / 256.0;  // dense fp32 MFMA per CU per second
-    const double slot_flops = cu_flops * efficiency / static_cast<double>(per_cu);
+    const double slot_flops = cu_flops * efficiency * occupancy / static_cast<double>(resident);
     double t = static_cast<double>(p.steps) * 2.0 * bm * bn * bk / slot_flops;
     if (p.partial_tiles > 0.0) t += (p.partial_tiles + 1.0) * m * n * 4.0 / 5.0e12;
     return t;
+}
+
+// Workgroups per CU a tile configuration is planned for: as many as fit the
+// 160 KB of LDS, except that a configuration of 8 waves already gives each
+// SIMD two waves with one workgroup, so it is planned one per CU.
+template <class Cfg>
+constexpr uint64_t plan_per_cu() {
+    return Cfg::kWaves >= 8 ? 1 : std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT>
@@ -623,9 +639,7 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (tiles >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: too many tiles");
-    // Resident workgroups per CU: as many tiles as fit the 160 KB of LDS.
-    const uint64_t per_cu = std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
-    const uint64_t slots = per_cu * (ctx->compute_units ? ctx->compute_units : 256);
+    const uint64_t slots = plan_per_cu<Cfg>() * (ctx->compute_units ? ctx->compute_units : 256);
     const GemmPlan plan = plan_gemm(m, k, n, BM, BN, BK, slots);
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
@@ -1206,15 +1220,24 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
-    // 256 x 256 tiles (8 waves of 64 x 128: twice the MFMA work per byte of
-    // LDS traffic, measured at ~81 % of peak against ~70 % for 128 x 128)
-    // wherever the model expects them to finish first, split-k included.
+    // Three tile configurations, picked by the time model per shape:
+    //  - 256 x 256 tiles, 8 waves of 64 x 128 (twice the MFMA work per byte of
+    //    LDS traffic): large products, ~88 % of peak at 4096^3;
+    //  - 128 x 128 tiles, 4 waves of 64 x 64, two workgroups per CU: products
+    //    whose tiles fill the CUs twice over (~82 % at 4096^3);
+    //  - 128 x 128 tiles, 8 waves of 32 x 64: products with about one tile
+    //    (or k split) per CU, where the 4-wave kernel leaves each SIMD one
+    //    wave (1024^3: 64 tiles x 4 k splits).
     using Big = TileCfg<256, 256, 32, 64, 128, false, false>;
     using Small = TileCfg<128, 128, 32, 64, 64, false, false>;
-    // Efficiencies measured at 4096^3 with each configuration: 88 % and 82 %.
-    const bool big = gemm_seconds(ctx, m, k, n, 256, 256, 32, Big::kLdsFloats * sizeof(float), 0.88) <
-                     gemm_seconds(ctx, m, k, n, 128, 128, 32, Small::kLdsFloats * sizeof(float), 0.82);
-    if (big) {
+    using Mid = TileCfg<128, 128, 32, 32, 64, false, false>;
+    const double t_big = gemm_seconds(ctx, m, k, n, 256, 256, 32, plan_per_cu<Big>(), Big::kWaves, 0.88);
+    const double t_small =
+        gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<Small>(), Small::kWaves, 0.82);
+    // Efficiencies measured at 4096^3 with each configuration forced: 88, 82
+    // and 83 % of peak.
+    const double t_mid = gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<Mid>(), Mid::kWaves, 0.83);
+    if (t_big < t_small && t_big <= t_mid) {
         if (!ta && !tb)
             return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
         if (ta && !tb)
@@ -1222,6 +1245,15 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         if (!ta && tb)
             return launch_mfma<256, 256, 32, 64, 128, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
         return launch_mfma<256, 256, 32, 64, 128, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+    }
+    if (t_mid < t_small) {
+        if (!ta && !tb)
+            return launch_mfma<128, 128, 32, 32, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        if (ta && !tb)
+            return launch_mfma<128, 128, 32, 32, 64, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        if (!ta && tb)
+            return launch_mfma<128, 128, 32, 32, 64, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        return launch_mfma<128, 128, 32, 32, 64, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
     }
     if (!ta && !tb)
         return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);

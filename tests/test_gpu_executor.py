@@ -332,3 +332,28 @@ def test_gated_matmul_is_bit_identical_to_its_parts(ex, orc, rows):
     assert_bitexact(ex.read_tensor("g.out"), want)
     for name in ("g.x", "g.w", "g.u", "g.gate", "g.up", "g.want", "g.out"):
         ex.release_tensor(name)
+
+
+def test_out_of_device_memory_is_triggered_by_a_real_over_capacity_allocation(dev, ex):
+    """src/tests.rs:47-71: an allocation of 64x the device's total memory
+    fails as OutOfDeviceMemory (mapped as src/error.rs:97-133); through the
+    executor the same failure is KernelOutOfDeviceMemory. Both leave the
+    context usable."""
+    import ctypes
+    from magnetar_hip import KernelError, _lib
+    total = dev.info()["total_memory"]
+    ptr = ctypes.c_void_p()
+    st = _lib.lib().mhip_alloc(dev.ctx, total * 64, ctypes.byref(ptr))
+    assert st == 5 and not ptr.value  # MHIP_OUT_OF_DEVICE_MEMORY
+    assert _lib.lib().mhip_status_name(st).decode() == "OutOfDeviceMemory"
+    assert "device bytes" in _lib.lib().mhip_last_error_detail().decode()
+    with pytest.raises(KernelError) as err:
+        ex.write_zeroed_tensor("oom.impossible", (total * 64 // 4,))
+    assert err.value.code == "KernelOutOfDeviceMemory"
+    # The context still allocates and runs.
+    ex.write_tensor("oom.after", np.arange(8, dtype=np.float32).reshape(2, 4))
+    ex.execute(inv("silu", ["oom.after"], "oom.after.silu"))
+    assert ex.read_tensor("oom.after.silu").shape == (2, 4)
+    st = _lib.lib().mhip_alloc(dev.ctx, 1024, ctypes.byref(ptr))
+    assert st == 0 and ptr.value
+    _lib.check(_lib.lib().mhip_free(dev.ctx, ptr))

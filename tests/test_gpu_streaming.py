@@ -175,9 +175,10 @@ def test_half_reference_fixtures(dev, orc):
 @pytest.mark.parametrize("dname", ["f16", "bf16"])
 @pytest.mark.parametrize("op", ["add", "mul"])
 def test_half_random_bit_patterns(dev, orc, dname, op):
-    """Uniformly random 16-bit patterns (subnormals, infinities and NaNs included).
-    Non-NaN results must match bit for bit; NaN results must be NaN (their
-    payload is the arithmetic unit's choice, which differs between CPUs)."""
+    """Uniformly random 16-bit patterns (subnormals, infinities and NaNs
+    included), bit for bit: NaN results too, whose payload follows the
+    reference CPU's x86-64 arithmetic (a NaN operand's, quieted, the second's
+    when both are NaN; the negative default NaN from inf - inf or 0 * inf)."""
     dt = HALF[dname]
     rng = np.random.default_rng(11 + dt)
     n = (1 << 22) + 5
@@ -186,8 +187,8 @@ def test_half_random_bit_patterns(dev, orc, dname, op):
     got = ops_half(dev, ha, hb, op, dt)
     want = orc.half_binary(ha, hb, dt, op)
     nan_w = is_half_nan(want, dt)
-    assert np.array_equal(is_half_nan(got, dt), nan_w)
-    assert_bitexact(got[~nan_w], want[~nan_w], f"{op}-{dname}")
+    assert nan_w.sum() > 1000  # NaN payloads are exercised
+    assert_bitexact(got, want, f"{op}-{dname}")
 
 
 def ops_half(dev, ha, hb, op, dt):
@@ -215,9 +216,7 @@ def test_half_all_pairs_of_one_operand(dev, orc, dname):
         for op in ("add", "mul"):
             got = ops_half(dev, all_bits, hb, op, dt)
             want = orc.half_binary(all_bits, hb, dt, op)
-            nan_w = is_half_nan(want, dt)
-            assert np.array_equal(is_half_nan(got, dt), nan_w)
-            assert_bitexact(got[~nan_w], want[~nan_w], f"{op}-{dname} partner={p:#x}")
+            assert_bitexact(got, want, f"{op}-{dname} partner={p:#x}")
 
 
 @pytest.mark.parametrize("dname", ["f16", "bf16"])

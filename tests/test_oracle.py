@@ -170,6 +170,23 @@ def test_half_arithmetic_against_numpy(orc, dt, op):
     assert_bitexact(got, want)
 
 
+def test_half_nan_payload_rule_known_answers(orc):
+    """The NaN rule the oracle states (x86-64 compiled f32 arithmetic): a NaN
+    operand's payload, quieted, the second operand's when both are NaN; the
+    negative default NaN from inf - inf or 0 * inf. The numpy comparison above
+    checks it over random patterns."""
+    def one(a, b, dt, op):
+        return int(orc.half_binary(np.array([a], np.uint16), np.array([b], np.uint16), dt, op)[0])
+    one_f16 = 0x3C00
+    assert one(0x7C01, one_f16, 0, "add") == 0x7E01   # signalling payload 1, quieted
+    assert one(one_f16, 0xFD00, 0, "add") == 0xFF00   # the second operand's, sign kept
+    assert one(0x7C01, 0xFD00, 0, "mul") == 0xFF00    # both NaN: the second
+    assert one(0xFD00, 0x7C01, 0, "mul") == 0x7E01
+    assert one(0x7C00, 0xFC00, 0, "add") == 0xFE00    # inf - inf: negative default NaN
+    assert one(0x7F80, 0x0000, 1, "mul") == 0xFFC0    # bf16 inf * 0
+    assert one(0x7F81, 0x3F80, 1, "add") == 0x7FC1    # bf16 signalling payload, quieted
+
+
 def test_half_golden(orc, fx):
     h = fx["half"]
     for name, dt in (("f16", 0), ("bf16", 1)):
