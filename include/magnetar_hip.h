@@ -186,6 +186,27 @@ mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float
                             uint64_t m, uint64_t k, uint64_t n, int transpose_a,
                             int transpose_b, const float* addend, int addend_mode);
 
+/* Which kernel path mhip_matmul_f32 takes for an m x k x n product with
+ * 16-byte aligned operands. No counterpart in the reference: a diagnostic for
+ * tests (that a case exercises the path it is written for) and tuning.
+ * path: the split-k GEMV (m <= 8), row blocks of 8 on the GEMV (16-32 rows of
+ * a small product), or MFMA tiles of tile_m x tile_n with `waves` waves per
+ * workgroup. splits: k slices of the GEMV, or k splits of the tiles (1: none);
+ * stream_k: 1 when (tile, k slice) runs are dealt to the workgroups. */
+enum {
+    MHIP_MATMUL_PATH_GEMV = 0,
+    MHIP_MATMUL_PATH_GEMV_ROW_BLOCKS = 1,
+    MHIP_MATMUL_PATH_TILES = 2
+};
+typedef struct {
+    uint32_t path;
+    uint32_t tile_m, tile_n, waves;
+    uint32_t splits;
+    uint32_t stream_k;
+} mhip_matmul_plan;
+mhip_status mhip_matmul_plan_f32(mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n,
+                                 int transpose_a, int transpose_b, mhip_matmul_plan* plan);
+
 /* ---- attention (src/kernels.rs:6505-7078; src/kernels.cu:1868-2787) ---- */
 typedef struct {
     uint64_t seq_len;           /* query rows */

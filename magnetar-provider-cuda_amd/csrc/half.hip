@@ -96,6 +96,52 @@ __device__ __forceinline__ uint32_t op2(uint32_t a, uint32_t b) {
     return op1<DT, OP>(a & 0xFFFFu, b & 0xFFFFu) | (op1<DT, OP>(a >> 16, b >> 16) << 16);
 }
 
+// The same operation when neither operand is infinite or NaN: the sum or
+// product of two finite halves is finite or overflows to infinity in f32, so
+// no NaN arises and the codec's NaN handling drops out. The results are
+// those of op1 bit for bit.
+template <int DT, int OP>
+__device__ __forceinline__ uint32_t op1_finite(uint32_t a, uint32_t b) {
+    float x, y;
+    if constexpr (DT == MHIP_BF16) {
+        x = bf16_decode(a);
+        y = bf16_decode(b);
+    } else {
+        x = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a)));
+        y = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+    }
+    const float r = materialize(OP ? x * y : x + y);
+    if constexpr (DT == MHIP_BF16) {
+        const uint32_t bits = __builtin_bit_cast(uint32_t, r);
+        return (bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16;
+    } else {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(r));
+    }
+}
+
+template <int DT, int OP>
+__device__ __forceinline__ uint32_t op2_finite(uint32_t a, uint32_t b) {
+    return op1_finite<DT, OP>(a & 0xFFFFu, b & 0xFFFFu) |
+           (op1_finite<DT, OP>(a >> 16, b >> 16) << 16);
+}
+
+// Whether any of the 16 halves of two 16-byte vectors has an all-ones
+// exponent (infinity or NaN). Each half's exponent field, masked in place,
+// is at most the all-ones pattern and equals it only for those values, so
+// the lane-wise maximum of the masked fields over the eight words shows it.
+template <int DT>
+__device__ __forceinline__ bool any_special(const uint4& a, const uint4& b) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    constexpr uint32_t kExp = DT == MHIP_BF16 ? 0x7F807F80u : 0x7C007C00u;
+    auto field = [](uint32_t w) { return __builtin_bit_cast(u16x2, w & kExp); };
+    const u16x2 ma = __builtin_elementwise_max(__builtin_elementwise_max(field(a.x), field(a.y)),
+                                               __builtin_elementwise_max(field(a.z), field(a.w)));
+    const u16x2 mb = __builtin_elementwise_max(__builtin_elementwise_max(field(b.x), field(b.y)),
+                                               __builtin_elementwise_max(field(b.z), field(b.w)));
+    const u16x2 m = __builtin_elementwise_max(ma, mb);
+    return m.x == (kExp & 0xFFFFu) || m.y == (kExp & 0xFFFFu);
+}
+
 template <int DT, int OP>
 __global__ __launch_bounds__(kThreads) void half_binary_kernel(const uint16_t* __restrict__ a,
                                                                const uint16_t* __restrict__ b,
@@ -120,10 +166,17 @@ __global__ __launch_bounds__(kThreads) void half_binary_kernel(const uint16_t* _
         uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
         if (i < full) {
             uint4 r;
-            r.x = op2<DT, OP>(va[u].x, vb[u].x);
-            r.y = op2<DT, OP>(va[u].y, vb[u].y);
-            r.z = op2<DT, OP>(va[u].z, vb[u].z);
-            r.w = op2<DT, OP>(va[u].w, vb[u].w);
+            if (!any_special<DT>(va[u], vb[u])) {
+                r.x = op2_finite<DT, OP>(va[u].x, vb[u].x);
+                r.y = op2_finite<DT, OP>(va[u].y, vb[u].y);
+                r.z = op2_finite<DT, OP>(va[u].z, vb[u].z);
+                r.w = op2_finite<DT, OP>(va[u].w, vb[u].w);
+            } else {
+                r.x = op2<DT, OP>(va[u].x, vb[u].x);
+                r.y = op2<DT, OP>(va[u].y, vb[u].y);
+                r.z = op2<DT, OP>(va[u].z, vb[u].z);
+                r.w = op2<DT, OP>(va[u].w, vb[u].w);
+            }
             mhip::store_nt(o4 + i, r);
         } else if (i == full) {
             for (uint64_t e = full * 8; e < n; ++e)

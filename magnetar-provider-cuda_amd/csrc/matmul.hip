@@ -75,10 +75,14 @@ mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
 // MFMA tiles
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T>
+// KG: the waves form KG groups that each cover the whole tile over every
+// KG-th part of each slice's k (summed in LDS at the end), so a small tile
+// still gives each SIMD two waves.
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, int KG = 1>
 struct TileCfg {
     static constexpr int kWavesN = BN / WN;
-    static constexpr int kWaves = (BM / WM) * kWavesN;
+    static constexpr int kTileWaves = (BM / WM) * kWavesN;
+    static constexpr int kWaves = kTileWaves * KG;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kMI = WM / 32;
     static constexpr int kNI = WN / 32;
@@ -88,7 +92,13 @@ struct TileCfg {
     // have their 16-byte chunks XOR-swizzled; rows along k are plain.
     static constexpr int kLdsA = BM * BK;
     static constexpr int kLdsB = BK * BN;
-    static constexpr int kLdsFloats = 2 * (kLdsA + kLdsB);
+    // Tiles of at most 64 x 64 give a wave only 8 MFMAs per slice, too few
+    // to cover a barrier and the first LDS reads of each slice: they move in
+    // steps of kGroup slices (one barrier per step), double-buffered, so
+    // kStages = 2 * kGroup slice buffers per operand.
+    static constexpr int kGroup = BM * BN <= 64 * 64 ? 4 : 1;
+    static constexpr int kStages = 2 * kGroup;
+    static constexpr int kLdsFloats = kStages * (kLdsA + kLdsB);
     // Global slices as (rows x cols) with cols contiguous in memory.
     static constexpr int kARows = A_T ? BK : BM, kACols = A_T ? BM : BK;
     static constexpr int kBRows = B_T ? BN : BK, kBCols = B_T ? BK : BN;
@@ -97,6 +107,9 @@ struct TileCfg {
     static_assert(kARows * kACols % (4 * kThreads) == 0, "A slice must split evenly");
     static_assert(kBRows * kBCols % (4 * kThreads) == 0, "B slice must split evenly");
     static_assert(BK == 32, "swizzled rows hold 8 chunks");
+    static_assert(KG == 1 || KG == 2 || KG == 4, "k groups split a slice's 4 groups of 8");
+    static_assert(KG == 1 || kTileWaves * kMI * kNI * 16 * 64 <= kLdsFloats,
+                  "the k groups' sums are staged in the slice buffers");
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -213,6 +226,14 @@ __device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t 
     }
 }
 
+// Workgroup barrier of the stepped pipeline, where LDS is written only by
+// direct loads that each issuing wave has already waited for: s_barrier
+// without the release fence of __syncthreads (whose waits are done). Every
+// LDS read of the previous step has returned (its MFMA was issued) before a
+// wave arrives. The memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void step_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
+
 // Maps the linear workgroup id to a (tile_m, tile_n): each XCD (ids are
 // dealt round-robin over 8) takes a contiguous band, and inside a band tiles
 // go down groups of 8 tile rows so neighbours share A rows and B columns.
@@ -235,24 +256,26 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
 // written to out[(row - out_r0) * ldo + (col - out_c0)] for the rows < M and
 // columns < N, plus the addend when addend_mode is 1 or 2. LDS (`lds`) is
 // free on entry and again on return.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG = 1>
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT* __restrict__ B,
                                           uint64_t M, uint64_t K, uint64_t N, uint64_t m0,
                                           uint64_t n0, uint64_t k_begin, uint64_t k_end,
                                           float* lds, float* __restrict__ out, uint64_t out_r0,
                                           uint64_t out_c0, uint64_t ldo,
                                           const float* __restrict__ addend, int addend_mode) {
-    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
+    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>;
     constexpr int T = Cfg::kThreads;
     // A rows along m (not A_T) and B rows along n (B_T) are swizzled.
     constexpr bool kASwz = !A_T, kBSwz = B_T;
     constexpr bool kBDma = std::is_same<BT, float>::value;  // compact B is widened on the way
-    // Buffer b of the A slices at lds + b * kLdsA; the B slices follow both.
-    float* const lds_b0 = lds + 2 * Cfg::kLdsA;
+    // Buffer b of the A slices at lds + b * kLdsA; the B slices follow them all.
+    float* const lds_b0 = lds + Cfg::kStages * Cfg::kLdsA;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int wm = wave / Cfg::kWavesN, wn = wave % Cfg::kWavesN;
+    const int kg = wave / Cfg::kTileWaves;  // this wave's k group
+    const int wt = wave % Cfg::kTileWaves;
+    const int wm = wt / Cfg::kWavesN, wn = wt % Cfg::kWavesN;
     const int lrow = lane & 31, lk = lane >> 5;
 
     v16f acc[Cfg::kMI][Cfg::kNI];
@@ -332,8 +355,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     auto compute = [&](int buf) {
         const float* la = lds + buf * Cfg::kLdsA;
         const float* lb = lds_b0 + buf * Cfg::kLdsB;
+        constexpr int kGroups = BK / 8 / KG;  // groups of 8 k per wave and slice
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
+        for (int gg = 0; gg < kGroups; ++gg) {
+            const int g = kg * kGroups + gg;
             mhip::f32x4 a4[Cfg::kMI], b4[Cfg::kNI];
             if constexpr (kASwz) {
 #pragma unroll
@@ -371,16 +396,71 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     };
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
-    issue(k_begin, 0);
-    finish(k_begin, 0);
-    __syncthreads();
-    for (uint64_t s = 0; s < slices; ++s) {
-        const int buf = static_cast<int>(s & 1);
-        const uint64_t k_next = k_begin + (s + 1) * BK;
-        if (s + 1 < slices) issue(k_next, buf ^ 1);
-        compute(buf);
-        if (s + 1 < slices) finish(k_next, buf ^ 1);
+    constexpr int G = Cfg::kGroup;
+    if (G > 1 && kBDma && interior_tile && (k_end - k_begin) % BK == 0) {
+        // Every slice goes straight to LDS. Steps of G slices, double-
+        // buffered: at step t the DMA waves wait for step t's loads, the
+        // barrier publishes them and frees the other buffer set (read in
+        // step t - 1), which then takes step t + 1 while step t computes.
+        const uint64_t steps = (slices + G - 1) / G;
+        auto issue_step = [&](uint64_t t) {
+            const int set = static_cast<int>(t & 1) * G;
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+                if (t * G + j < slices) issue(k_begin + (t * G + j) * BK, set + j);
+        };
+        issue_step(0);
+        for (uint64_t t = 0; t < steps; ++t) {
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of step t have landed
+            step_barrier();
+            if (t + 1 < steps) issue_step(t + 1);
+            const int set = static_cast<int>(t & 1) * G;
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+                if (t * G + j < slices) compute(set + j);
+        }
         __syncthreads();
+    } else {
+        issue(k_begin, 0);
+        finish(k_begin, 0);
+        __syncthreads();
+        for (uint64_t s = 0; s < slices; ++s) {
+            const int buf = static_cast<int>(s & 1);
+            const uint64_t k_next = k_begin + (s + 1) * BK;
+            if (s + 1 < slices) issue(k_next, buf ^ 1);
+            compute(buf);
+            if (s + 1 < slices) finish(k_next, buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // k groups: the others' sums meet group 0's in LDS (free after the loop's
+    // last barrier), added in group order; group 0 writes the tile.
+    if constexpr (KG > 1) {
+        constexpr int kPer = Cfg::kMI * Cfg::kNI * 16 * 64;  // floats per wave
+        for (int q = 1; q < KG; ++q) {
+            if (kg == q) {
+#pragma unroll
+                for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::kNI; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            lds[wt * kPer + ((i * Cfg::kNI + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (kg == 0) {
+#pragma unroll
+                for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::kNI; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[i][j][r] += lds[wt * kPer + ((i * Cfg::kNI + j) * 16 + r) * 64 + lane];
+            }
+            __syncthreads();  // LDS is free again
+        }
+        if (kg != 0) return;
     }
 
     // Accumulator r of lane l holds C[8*(r/4) + 4*(l/32) + r%4][l%32] of its 32x32 block.
@@ -408,8 +488,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
 // [y * k_split, min(K, (y + 1) * k_split)) and, with more than one split,
 // writes that partial product to C + y * M * N (no addend) for
 // splitk_reduce_kernel.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
-__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_kernel(
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThreads), 2) void mfma_gemm_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
     uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
     extern __shared__ float lds[];
@@ -420,7 +500,7 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
     const uint64_t k_end = min(K, k_begin + k_split);
     const bool split = gridDim.y > 1;
     float* out = split ? C + static_cast<uint64_t>(blockIdx.y) * M * N : C;
-    gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT>(
+    gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG>(
         A, B, M, K, N, static_cast<uint64_t>(tm) * BM, static_cast<uint64_t>(tn) * BN, k_begin,
         k_end, lds, out, 0, 0, N, addend, split ? 0 : addend_mode);
 }
@@ -431,8 +511,8 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
 // Workgroup w covers units [w * per, (w + 1) * per); per <= slices per tile,
 // so that run touches at most two tiles, and the part of the j-th one goes to
 // slot 2w + j as a BM x BN tile for stream_reduce_kernel.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT>
-__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 2) void mfma_gemm_stream_kernel(
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThreads), 2) void mfma_gemm_stream_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ slots, uint64_t M,
     uint64_t K, uint64_t N, uint64_t per) {
     extern __shared__ float lds[];
@@ -446,7 +526,7 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T>::kThreads), 
         const uint64_t s1 = min(kslices, s0 + (end - u));
         const uint64_t m0 = t / tiles_n * BM, n0 = t % tiles_n * BN;
         float* slot = slots + (2 * static_cast<uint64_t>(blockIdx.x) + seg) * (BM * BN);
-        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT>(A, B, M, K, N, m0, n0, s0 * BK,
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG>(A, B, M, K, N, m0, n0, s0 * BK,
                                                          min(K, s1 * BK), lds, slot, m0, n0, BN,
                                                          nullptr, 0);
         u += s1 - s0;
@@ -603,7 +683,8 @@ GemmPlan plan_gemm(uint64_t m, uint64_t k, uint64_t n, uint64_t bm, uint64_t bn,
 
 // Estimated seconds for an m x k x n product with one tile configuration:
 // the critical path's k slices at the configuration's measured fraction of
-// peak, plus the partial results' traffic. Splits are planned for
+// peak, plus the partial results' traffic, plus a fixed cost per launch (a
+// k split or stream-K adds the reduction's). Splits are planned for
 // `plan_per_cu` workgroups per CU. The workgroups resident on a CU share its
 // MFMA pipes; below two waves per SIMD a wave's LDS reads are exposed, so
 // the fraction scales with waves per SIMD / 2 (one 4-wave workgroup per CU
@@ -620,8 +701,11 @@ double gemm_seconds(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n, uin
     const double occupancy = std::min(1.0, per_simd / 2.0);
     const double cu_flops = 157.3e12 / 256.0;  // dense fp32 MFMA per CU per second
     const double slot_flops = cu_flops * efficiency * occupancy / static_cast<double>(resident);
-    double t = static_cast<double>(p.steps) * 2.0 * bm * bn * bk / slot_flops;
-    if (p.partial_tiles > 0.0) t += (p.partial_tiles + 1.0) * m * n * 4.0 / 5.0e12;
+    // A dependent launch costs about 4 us on this device even when it moves
+    // little (start-up, the first memory latency, end-of-kernel cache work).
+    constexpr double kLaunchSeconds = 4.0e-6;
+    double t = static_cast<double>(p.steps) * 2.0 * bm * bn * bk / slot_flops + kLaunchSeconds;
+    if (p.partial_tiles > 0.0) t += (p.partial_tiles + 1.0) * m * n * 4.0 / 5.0e12 + kLaunchSeconds;
     return t;
 }
 
@@ -633,10 +717,10 @@ constexpr uint64_t plan_per_cu() {
     return Cfg::kWaves >= 8 ? 1 : std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT, int KG = 1>
 mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
                         uint64_t k, uint64_t n, const float* addend, int mode, bool vec) {
-    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T>;
+    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (tiles >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: too many tiles");
     const uint64_t slots = plan_per_cu<Cfg>() * (ctx->compute_units ? ctx->compute_units : 256);
@@ -644,10 +728,10 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
     if (!configured) {
-        for (const void* f : {reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
-                              reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>),
-                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>),
-                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>)})
+        for (const void* f : {reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>),
+                              reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>)})
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
@@ -662,10 +746,10 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
         if (st != MHIP_OK) return st;
         const dim3 grid(static_cast<unsigned>(plan.groups));
         if (vec)
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>), grid,
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>), grid,
                                dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
         else
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>), grid,
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>), grid,
                                dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
         st = mhip::check_launch("matmul (MFMA stream-K)");
         if (st != MHIP_OK) return st;
@@ -682,11 +766,11 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(plan.splits));
     if (vec)
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, plan.k_split);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, plan.k_split);
     mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
@@ -1189,6 +1273,74 @@ __global__ void fill_addend_kernel(float* C, uint64_t M, uint64_t N, const float
 
 // The shared body of the f32 and compact-weight matmuls: B as f32 or as bf16
 // bit patterns; everything else (A, C, the addend, the arithmetic) is f32.
+// The tile configurations, picked per shape by the time model (efficiencies
+// measured with each configuration forced):
+//  - kBig: 256 x 256 tiles, 8 waves of 64 x 128 (twice the MFMA work per byte
+//    of LDS traffic): large products, 88 % of peak at 4096^3;
+//  - kSmall: 128 x 128 tiles, 4 waves of 64 x 64, two workgroups per CU:
+//    products whose tiles fill the CUs twice over (82 % at 4096^3);
+//  - kMid: 128 x 128 tiles, 8 waves of 32 x 64: products with about one tile
+//    (or k split) per CU, where the 4-wave kernel leaves each SIMD one wave
+//    (83 % at 4096^3);
+//  - kTiny: 64 x 64 tiles, 8 waves of 32 x 32 in two k groups, four-slice
+//    steps: products of about one such tile per CU (1024^3: 256 tiles),
+//    which then need no k split and no second launch (about 65 % of peak in
+//    its steady state, measured per step with s_memtime at 1024^3).
+enum class TileChoice { kBig, kSmall, kMid, kTiny };
+
+using BigCfg = TileCfg<256, 256, 32, 64, 128, false, false>;
+using SmallCfg = TileCfg<128, 128, 32, 64, 64, false, false>;
+using MidCfg = TileCfg<128, 128, 32, 32, 64, false, false>;
+using TinyCfg = TileCfg<64, 64, 32, 32, 32, false, false, 2>;
+
+TileChoice choose_tiles(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n) {
+    const double t_big = gemm_seconds(ctx, m, k, n, 256, 256, 32, plan_per_cu<BigCfg>(), BigCfg::kWaves, 0.88);
+    const double t_small =
+        gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<SmallCfg>(), SmallCfg::kWaves, 0.82);
+    const double t_mid = gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<MidCfg>(), MidCfg::kWaves, 0.83);
+    const double t_tiny = gemm_seconds(ctx, m, k, n, 64, 64, 32, plan_per_cu<TinyCfg>(), TinyCfg::kWaves, 0.65);
+    if (t_tiny < t_big && t_tiny < t_small && t_tiny < t_mid) return TileChoice::kTiny;
+    if (t_big < t_small && t_big <= t_mid) return TileChoice::kBig;
+    if (t_mid < t_small) return TileChoice::kMid;
+    return TileChoice::kSmall;
+}
+
+// Which kernel path a product takes (the decode GEMV rules of matmul_impl,
+// then the tile choice); `b_aligned`: B's base allows its vector loads.
+mhip_matmul_plan plan_matmul(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n, bool ta,
+                             bool tb, bool b_aligned) {
+    mhip_matmul_plan out{};
+    if (m <= kGemvMaxRows && !ta && !tb && n % 4 == 0 && b_aligned) {
+        uint64_t slices, per;
+        gemv_slicing(ctx, k, n, &slices, &per);
+        out.path = MHIP_MATMUL_PATH_GEMV;
+        out.splits = static_cast<uint32_t>(slices);
+        return out;
+    }
+    if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= kGemvSmallProduct && !ta &&
+        !tb && n % 4 == 0 && b_aligned) {
+        uint64_t slices, per;
+        gemv_slicing(ctx, k, n, &slices, &per);
+        out.path = MHIP_MATMUL_PATH_GEMV_ROW_BLOCKS;
+        out.splits = static_cast<uint32_t>(slices);
+        return out;
+    }
+    out.path = MHIP_MATMUL_PATH_TILES;
+    uint64_t bm = 128, waves = SmallCfg::kWaves, per_cu = plan_per_cu<SmallCfg>();
+    switch (choose_tiles(ctx, m, k, n)) {
+        case TileChoice::kBig: bm = 256; waves = BigCfg::kWaves; per_cu = plan_per_cu<BigCfg>(); break;
+        case TileChoice::kMid: waves = MidCfg::kWaves; per_cu = plan_per_cu<MidCfg>(); break;
+        case TileChoice::kTiny: bm = 64; waves = TinyCfg::kWaves; per_cu = plan_per_cu<TinyCfg>(); break;
+        case TileChoice::kSmall: break;
+    }
+    const GemmPlan p = plan_gemm(m, k, n, bm, bm, 32, per_cu * (ctx->compute_units ? ctx->compute_units : 256));
+    out.tile_m = out.tile_n = static_cast<uint32_t>(bm);
+    out.waves = static_cast<uint32_t>(waves);
+    out.splits = p.stream ? 1u : static_cast<uint32_t>(p.splits);
+    out.stream_k = p.stream ? 1u : 0u;
+    return out;
+}
+
 template <class BT>
 mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, uint64_t m,
                         uint64_t k, uint64_t n, int transpose_a, int transpose_b,
@@ -1220,40 +1372,33 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
-    // Three tile configurations, picked by the time model per shape:
-    //  - 256 x 256 tiles, 8 waves of 64 x 128 (twice the MFMA work per byte of
-    //    LDS traffic): large products, ~88 % of peak at 4096^3;
-    //  - 128 x 128 tiles, 4 waves of 64 x 64, two workgroups per CU: products
-    //    whose tiles fill the CUs twice over (~82 % at 4096^3);
-    //  - 128 x 128 tiles, 8 waves of 32 x 64: products with about one tile
-    //    (or k split) per CU, where the 4-wave kernel leaves each SIMD one
-    //    wave (1024^3: 64 tiles x 4 k splits).
-    using Big = TileCfg<256, 256, 32, 64, 128, false, false>;
-    using Small = TileCfg<128, 128, 32, 64, 64, false, false>;
-    using Mid = TileCfg<128, 128, 32, 32, 64, false, false>;
-    const double t_big = gemm_seconds(ctx, m, k, n, 256, 256, 32, plan_per_cu<Big>(), Big::kWaves, 0.88);
-    const double t_small =
-        gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<Small>(), Small::kWaves, 0.82);
-    // Efficiencies measured at 4096^3 with each configuration forced: 88, 82
-    // and 83 % of peak.
-    const double t_mid = gemm_seconds(ctx, m, k, n, 128, 128, 32, plan_per_cu<Mid>(), Mid::kWaves, 0.83);
-    if (t_big < t_small && t_big <= t_mid) {
-        if (!ta && !tb)
-            return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        if (ta && !tb)
-            return launch_mfma<256, 256, 32, 64, 128, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        if (!ta && tb)
-            return launch_mfma<256, 256, 32, 64, 128, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        return launch_mfma<256, 256, 32, 64, 128, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-    }
-    if (t_mid < t_small) {
-        if (!ta && !tb)
-            return launch_mfma<128, 128, 32, 32, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        if (ta && !tb)
-            return launch_mfma<128, 128, 32, 32, 64, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        if (!ta && tb)
-            return launch_mfma<128, 128, 32, 32, 64, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
-        return launch_mfma<128, 128, 32, 32, 64, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+    switch (choose_tiles(ctx, m, k, n)) {
+        case TileChoice::kTiny:
+            if (!ta && !tb)
+                return launch_mfma<64, 64, 32, 32, 32, false, false, BT, 2>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (ta && !tb)
+                return launch_mfma<64, 64, 32, 32, 32, true, false, BT, 2>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (!ta && tb)
+                return launch_mfma<64, 64, 32, 32, 32, false, true, BT, 2>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            return launch_mfma<64, 64, 32, 32, 32, true, true, BT, 2>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        case TileChoice::kBig:
+            if (!ta && !tb)
+                return launch_mfma<256, 256, 32, 64, 128, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (ta && !tb)
+                return launch_mfma<256, 256, 32, 64, 128, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (!ta && tb)
+                return launch_mfma<256, 256, 32, 64, 128, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            return launch_mfma<256, 256, 32, 64, 128, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        case TileChoice::kMid:
+            if (!ta && !tb)
+                return launch_mfma<128, 128, 32, 32, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (ta && !tb)
+                return launch_mfma<128, 128, 32, 32, 64, true, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            if (!ta && tb)
+                return launch_mfma<128, 128, 32, 32, 64, false, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+            return launch_mfma<128, 128, 32, 32, 64, true, true, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
+        case TileChoice::kSmall:
+            break;
     }
     if (!ta && !tb)
         return launch_mfma<128, 128, 32, 64, 64, false, false, BT>(ctx, a, b, out, m, k, n, addend, addend_mode, vec);
@@ -1265,6 +1410,15 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
 }
 
 }  // namespace
+
+extern "C" mhip_status mhip_matmul_plan_f32(mhip_ctx* ctx, uint64_t m, uint64_t k, uint64_t n,
+                                            int transpose_a, int transpose_b,
+                                            mhip_matmul_plan* plan) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (!plan) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul plan: null output");
+    *plan = plan_matmul(ctx, m, k, n, transpose_a != 0, transpose_b != 0, true);
+    return MHIP_OK;
+}
 
 extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,
                                        uint64_t m, uint64_t k, uint64_t n, int transpose_a,

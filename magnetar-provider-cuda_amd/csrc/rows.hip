@@ -38,8 +38,10 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 }
 
 // Reduces over the G threads of this row's group. For G == 256 the four
-// waves meet in `scratch` (4 floats); every thread gets the result.
-template <int G, class Op>
+// waves meet in `scratch` (4 floats); every thread gets the result. REUSE:
+// the caller reduces through `scratch` again, so the reads of this call must
+// finish before the next call's writes (a second barrier).
+template <int G, class Op, bool REUSE = true>
 __device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
     v = wave_reduce(v, op);
     if constexpr (G == 256) {
@@ -47,7 +49,7 @@ __device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
         if ((threadIdx.x & 63) == 0) scratch[wave] = v;
         __syncthreads();
         v = op(op(scratch[0], scratch[1]), op(scratch[2], scratch[3]));
-        __syncthreads();
+        if constexpr (REUSE) __syncthreads();
     }
     return v;
 }
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
 #pragma unroll
     for (int v = 0; v < VPT; ++v)
         ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
-    ss = group_reduce<G>(ss, SumOp{}, scratch);
+    ss = group_reduce<G, SumOp, false>(ss, SumOp{}, scratch);
     if (!live) return;
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;

@@ -74,6 +74,15 @@ class RopeParams(ctypes.Structure):
     ]
 
 
+class MatmulPlan(ctypes.Structure):
+    """mhip_matmul_plan: the kernel path mhip_matmul_f32 takes for a shape."""
+    _fields_ = [("path", ctypes.c_uint32), ("tile_m", ctypes.c_uint32), ("tile_n", ctypes.c_uint32),
+                ("waves", ctypes.c_uint32), ("splits", ctypes.c_uint32), ("stream_k", ctypes.c_uint32)]
+
+
+MATMUL_PATHS = {0: "gemv", 1: "gemv_row_blocks", 2: "tiles"}
+
+
 class AttentionParams(ctypes.Structure):
     _fields_ = [
         ("seq_len", ctypes.c_uint64),
@@ -138,6 +147,7 @@ SIGNATURES = {
     "mhip_rope_f32": [_CTX, _P, _P, _U64, _U64, ctypes.POINTER(RopeParams)],
     "mhip_matmul_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
     "mhip_matmul_f32_noalloc": [_CTX, _P, _P, _P, _U64, _U64, _U64, _I, _I, _P, _I],
+    "mhip_matmul_plan_f32": [_CTX, _U64, _U64, _U64, _I, _I, ctypes.POINTER(MatmulPlan)],
     "mhip_attention_f32": [_CTX, _P, _P, _P, _P, ctypes.POINTER(AttentionParams)],
     "mhip_kv_write_f32": [_CTX, _P, _U64, _U64, _P, _U64, _U64],
     "mhip_matmul_bf16w_f32": [_CTX, _P, _P, _P, _U64, _U64, _U64, ctypes.c_int, ctypes.c_int, _P,

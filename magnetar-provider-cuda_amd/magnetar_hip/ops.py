@@ -138,6 +138,18 @@ def matmul(dev: Device, a: DeviceArray, b: DeviceArray, transpose_a: bool = Fals
     return out
 
 
+def matmul_plan(dev: Device, m: int, k: int, n: int, transpose_a: bool = False,
+                transpose_b: bool = False) -> dict:
+    """The kernel path mhip_matmul_f32 takes for an m x k x n product with
+    aligned operands: {"path": "gemv" | "gemv_row_blocks" | "tiles", "tile":
+    (tile_m, tile_n), "waves", "splits", "stream_k"}."""
+    p = _lib.MatmulPlan()
+    call("mhip_matmul_plan_f32", dev.ctx, m, k, n, int(transpose_a), int(transpose_b),
+         ctypes.byref(p))
+    return {"path": _lib.MATMUL_PATHS[p.path], "tile": (p.tile_m, p.tile_n), "waves": p.waves,
+            "splits": p.splits, "stream_k": bool(p.stream_k)}
+
+
 def attention_params(seq_len, kv_rows, head_count, head_dimension, kv_head_count=None,
                      value_dimension=None, causal=False, window_size=None, key_count=None,
                      scale=None, batch=1) -> _lib.AttentionParams:

@@ -113,6 +113,9 @@ def test_zero_inner_dimension(dev, orc):
     assert_bitexact(got, np.tile(bias, (3, 1)))
 
 
+SQUARE_TILES = {1024: (64, 64), 2048: (128, 128), 4096: (256, 256), 8192: (256, 256)}
+
+
 @pytest.mark.parametrize("size", [1024, 2048, 4096, 8192])
 def test_square_baseline_sizes(dev, orc, size):
     """BASELINE config 2's square products. 1024^3 against the whole oracle
@@ -123,6 +126,10 @@ def test_square_baseline_sizes(dev, orc, size):
     beside the normwise bar."""
     from magnetar_hip import ops
     from reference_chain import matmul as oracle_matmul
+    from magnetar_hip import ops as _ops
+    plan = _ops.matmul_plan(dev, size, size, size)
+    assert plan["path"] == "tiles" and plan["tile"] == SQUARE_TILES[size], plan
+    assert plan["splits"] == 1 and not plan["stream_k"], plan
     a = orc.uniform(size * size, 21, -1.0, 1.0).reshape(size, size)
     b = orc.uniform(size * size, 22, -1.0, 1.0).reshape(size, size)
     c = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
@@ -147,12 +154,14 @@ def test_square_baseline_sizes(dev, orc, size):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("m,k,n,mode", [(4100, 64, 4100, 0), (4096, 96, 4164, 1), (4164, 40, 4096, 2)])
+@pytest.mark.parametrize("m,k,n,mode", [(4000, 64, 4064, 0), (4000, 96, 4064, 1), (4064, 40, 4000, 2)])
 def test_large_tile_path_ragged_edges_and_addends(dev, orc, m, k, n, mode):
-    """Products with at least one 256 x 256 tile per CU take the 8-wave tile
-    kernel; ragged edges and both addend forms against the oracle, and the
-    fused addend bit-identical to matmul + add."""
+    """Products of about one 256 x 256 tile per CU take the 8-wave 256-tile
+    kernel (asserted); ragged edges and both addend forms against the oracle,
+    and the fused addend bit-identical to matmul + add."""
     from magnetar_hip import ops
+    plan = ops.matmul_plan(dev, m, k, n)
+    assert plan["tile"] == (256, 256) and plan["splits"] == 1 and not plan["stream_k"], plan
     a = orc.uniform(m * k, 31 + m, -1.0, 1.0).reshape(m, k)
     b = orc.uniform(k * n, 32 + n, -1.0, 1.0).reshape(k, n)
     addend = None
@@ -179,6 +188,8 @@ def test_row_blocked_gemv(dev, orc, m, k, n, mode):
     GEMV: against the oracle, and each block of 8 rows bit-identical to the
     8-row GEMV of those rows alone (same slicing of k, same summation order)."""
     from magnetar_hip import ops
+    assert ops.matmul_plan(dev, m, k, n)["path"] == "gemv_row_blocks"
+    assert ops.matmul_plan(dev, 8, k, n)["path"] == "gemv"
     a = orc.uniform(m * k, 41 + m, -1.0, 1.0).reshape(m, k)
     b = orc.uniform(k * n, 42 + n, -1.0, 1.0).reshape(k, n)
     addend = None
@@ -203,14 +214,21 @@ def test_row_blocked_gemv(dev, orc, m, k, n, mode):
         assert_bitexact(got[r:r + 8], block)
 
 
-@pytest.mark.parametrize("m,k,n,mode", [(400, 2050, 1900, 0), (400, 2050, 1900, 1), (130, 4096, 4000, 2),
-                                        (40, 4096, 4096, 1), (400, 2050, 1901, 2)])
-def test_stream_k_products(dev, orc, m, k, n, mode):
-    """Products whose tiles do not divide the device run stream-K (equal runs
-    of (tile, k slice) units per workgroup, partial tiles summed in k order):
-    ragged edges, a short last run, both tile sizes, against the oracle, and
-    the fused addend bit-identical to matmul + add."""
+@pytest.mark.parametrize("m,k,n,mode,tile,stream", [
+    (200, 2050, 1900, 0, 128, True), (200, 2050, 1900, 1, 128, True), (201, 2050, 1901, 2, 128, True),
+    (200, 4096, 2500, 1, 128, True), (130, 512, 3000, 2, 64, True),
+    (400, 1024, 1900, 2, 128, False), (130, 512, 1900, 1, 64, False), (40, 4096, 4096, 1, 64, False)])
+def test_stream_k_products(dev, orc, m, k, n, mode, tile, stream):
+    """Products whose tiles cannot fill the device split k: stream-K (equal
+    runs of (tile, k slice) units per workgroup, partial tiles summed in k
+    order) or whole k splits, on the 64-, and 128-tile kernels (the plan is
+    asserted; the 256-tile stream-K is the prefill projection below): ragged
+    edges, a short last run, against the oracle, deterministic, and the fused
+    addend bit-identical to matmul + add."""
     from magnetar_hip import ops
+    plan = ops.matmul_plan(dev, m, k, n)
+    assert plan["tile"] == (tile, tile) and plan["stream_k"] == stream, plan
+    assert stream or plan["splits"] > 1, plan
     a = orc.uniform(m * k, 51 + m, -1.0, 1.0).reshape(m, k)
     b = orc.uniform(k * n, 52 + n, -1.0, 1.0).reshape(k, n)
     addend = None
@@ -236,10 +254,12 @@ def test_stream_k_products(dev, orc, m, k, n, mode):
 
 def test_stream_k_prefill_projection(dev, orc):
     """The gate/up projection of a 512-token Llama-2-7B prefill (512 x 4096
-    x 11008, 86 tiles of 256 x 256): 16 sampled rows against the oracle and a
-    checksum of the whole product, C x = A (B x), in f64."""
+    x 11008, 86 tiles of 256 x 256, stream-K): 16 sampled rows against the
+    oracle and a checksum of the whole product, C x = A (B x), in f64."""
     from magnetar_hip import ops
     m, k, n = 512, 4096, 11008
+    plan = ops.matmul_plan(dev, m, k, n)
+    assert plan["tile"] == (256, 256) and plan["stream_k"], plan
     a = orc.uniform(m * k, 61, -1.0, 1.0).reshape(m, k)
     b = orc.uniform(k * n, 62, -1.0, 1.0).reshape(k, n)
     c = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
@@ -257,7 +277,8 @@ def test_large_tile_path_with_transposed_operands(dev, orc, ta, tb):
     ragged edges, against the oracle, and bit-identical to the same product
     with the operands stored untransposed (same tiles, same k order)."""
     from magnetar_hip import ops
-    m, k, n = 4100, 96, 4164
+    m, k, n = 4000, 96, 4064
+    assert ops.matmul_plan(dev, m, k, n, ta, tb)["tile"] == (256, 256)
     a = orc.uniform(m * k, 91, -1.0, 1.0).reshape(m, k)
     b = orc.uniform(k * n, 92, -1.0, 1.0).reshape(k, n)
     a_in = np.ascontiguousarray(a.T) if ta else a
