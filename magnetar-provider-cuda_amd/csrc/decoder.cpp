@@ -26,7 +26,7 @@
 namespace {
 
 struct Layout {
-    uint64_t x, h, q, a, x2, h2, g, u;  // float offsets into the workspace
+    uint64_t x, h, q, a, x2, h2, g, u, css;  // float offsets into the workspace
     uint64_t floats;
 };
 
@@ -46,6 +46,7 @@ Layout layout(const mhip_block_config& c, uint64_t seq) {
     l.h2 = take(seq * c.hidden);
     l.g = take(seq * c.ffn);
     l.u = take(seq * c.ffn);
+    l.css = take((c.hidden + 255) / 256);  // one token's RMSNorm chunk sums
     l.floats = off;
     return l;
 }
@@ -75,7 +76,7 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     if (workspace_bytes < l.floats * sizeof(float)) return MHIP_SHAPE_UNSUPPORTED;
     float* ws = static_cast<float*>(workspace);
     float *x = ws + l.x, *h = ws + l.h, *q = ws + l.q, *a = ws + l.a, *x2 = ws + l.x2,
-          *h2 = ws + l.h2, *g = ws + l.g, *u = ws + l.u;
+          *h2 = ws + l.h2, *g = ws + l.g, *u = ws + l.u, *css = ws + l.css;
     const uint64_t kv_dim = c.kv_heads * c.head_dim;
     float* k_rows = k_cache + position * kv_dim;
     float* v_rows = v_cache + position * kv_dim;
@@ -95,17 +96,6 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
         if ((st = (call)) != MHIP_OK) \
             return st;                 \
     } while (0)
-    // Embedding + RMSNorm in one pass where the row fits the fused kernel.
-    st = mhip::embed_rmsnorm_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, w->attn_norm,
-                                 c.eps, x, h, bf16);
-    if (st == MHIP_LAYOUT_UNSUPPORTED) {
-        MHIP_TRY(bf16 ? mhip_embedding_bf16w_f32(ctx, reinterpret_cast<const uint16_t*>(w->embedding),
-                                                 c.vocab, c.hidden, ids, seq, x)
-                      : mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
-        MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
-    } else if (st != MHIP_OK) {
-        return st;
-    }
     mhip_rope_params rope[2];
     mhip_rope_params_default(&rope[0], c.head_dim, c.heads);
     rope[0].base = c.rope_base;
@@ -121,6 +111,17 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     mhip::GemvTarget qkv[3] = {{w->wq, c.heads * c.head_dim, q},
                                {w->wk, kv_dim, k_rows, true, rows_left},
                                {w->wv, kv_dim, v_rows, true, rows_left}};
+    // Embedding + RMSNorm in one pass where the row fits the fused kernel.
+    st = mhip::embed_rmsnorm_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, w->attn_norm,
+                                 c.eps, x, h, bf16);
+    if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        MHIP_TRY(bf16 ? mhip_embedding_bf16w_f32(ctx, reinterpret_cast<const uint16_t*>(w->embedding),
+                                                 c.vocab, c.hidden, ids, seq, x)
+                      : mhip_embedding_f32(ctx, w->embedding, c.vocab, c.hidden, ids, seq, x));
+        MHIP_TRY(mhip_rmsnorm_f32(ctx, x, w->attn_norm, h, seq, c.hidden, 0, c.eps));
+    } else if (st != MHIP_OK) {
+        return st;
+    }
     st = mhip::gemv_set_f32(ctx, h, seq, c.hidden, qkv, 3, mhip::kGemvRopeQK, rope, bf16);
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
         // The separate matmuls write fixed rows of the cache.
@@ -148,12 +149,35 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     ap.window_size = -1;
     ap.batch = 1;
     MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
-    MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
-    MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
+    // One token: the O projection's reduction also writes x2's RMSNorm
+    // chunk sums, and the gate/up launch normalises x2 from them (no
+    // RMSNorm launch). Otherwise matmul-residual, then RMSNorm.
+    st = MHIP_LAYOUT_UNSUPPORTED;
+    if (seq == 1)
+        st = mhip::gemv_chunks_f32(ctx, a, w->wo, x2, c.heads * c.head_dim, c.hidden, x, 2, bf16, css);
+    if (st == MHIP_LAYOUT_UNSUPPORTED)
+        MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
+    else if (st != MHIP_OK)
+        return st;
+    const bool have_chunks = st == MHIP_OK && seq == 1;
     // Decode (as for Q/K/V): gate and up as one set of GEMVs whose reduction writes
     // silu(gate) * up. Otherwise two matmuls and silu-mul.
     const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};
-    st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr, bf16);
+    st = MHIP_LAYOUT_UNSUPPORTED;
+    if (have_chunks) {
+        mhip::RowNorm n{};
+        n.src = x2;
+        n.chunk_ss = css;
+        n.gain = w->ffn_norm;
+        n.eps = c.eps;
+        st = mhip::gemv_set_f32(ctx, nullptr, 1, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr,
+                                bf16, &n);
+        if (st != MHIP_OK && st != MHIP_LAYOUT_UNSUPPORTED) return st;
+    }
+    if (st == MHIP_LAYOUT_UNSUPPORTED) {
+        MHIP_TRY(mhip_rmsnorm_f32(ctx, x2, w->ffn_norm, h2, seq, c.hidden, 0, c.eps));
+        st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr, bf16);
+    }
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
         MHIP_TRY(mm(h2, w->w_gate, g, seq, c.hidden, c.ffn, nullptr, 0));
         MHIP_TRY(mm(h2, w->w_up, u, seq, c.hidden, c.ffn, nullptr, 0));

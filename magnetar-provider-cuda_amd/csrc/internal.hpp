@@ -50,9 +50,31 @@ enum GemvEpilogue : int {
 // MHIP_LAYOUT_UNSUPPORTED when a target does not fit the decode GEMV
 // (n % 4, alignment, rows > 8) or the rope parameters are not the vector
 // interleaved form; the caller then runs the separate calls.
+//
+// With `norm` (one row only), the input is not `a` but the row norm.src
+// normalised inside the partial launch: times its RMSNorm scale (from the
+// row's chunk sums of squares, norm.chunk_ss, as gemv_chunks_f32 writes them)
+// and gain -- the bits of mhip_rmsnorm_f32 followed by the set.
+struct RowNorm {
+    const float* src;
+    const float* chunk_ss;
+    const float* gain = nullptr;
+    float eps = 0.0f;
+};
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                          const GemvTarget* targets, int count, int epilogue,
-                         const mhip_rope_params* rope, bool bf16_weights = false);
+                         const mhip_rope_params* rope, bool bf16_weights = false,
+                         const RowNorm* norm = nullptr);
+
+// out[1, n] = a[1, k] . b[k, n] (+ addend as mhip_matmul_f32's addend_mode),
+// exactly the one-row decode GEMV of mhip_matmul_f32 (b f32, or bf16 bits
+// when `bf16_weights`), that also writes the RMSNorm chunk sums of squares of
+// `out` (mhip::chunk_sumsq; ceil(n / 256) floats) to chunk_ss. Returns
+// MHIP_LAYOUT_UNSUPPORTED when that GEMV would not split k (the chunk sums
+// come from its reduction launch) or the operands do not fit it.
+mhip_status gemv_chunks_f32(mhip_ctx* ctx, const float* a, const void* b, float* out, uint64_t k,
+                            uint64_t n, const float* addend, int addend_mode, bool bf16_weights,
+                            float* chunk_ss);
 
 // While capturing: records that `what` cannot be captured and returns
 // MHIP_CAPTURE_UNSUPPORTED; MHIP_OK otherwise.

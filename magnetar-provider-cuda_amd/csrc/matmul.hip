@@ -41,6 +41,7 @@
 
 #include <mutex>
 #include "internal.hpp"
+#include "reduce.hpp"
 
 namespace {
 
@@ -839,9 +840,23 @@ struct GemvLoad<uint16_t, 8> {
 // matrix larger than an XCD's L2, read once per call); a small B is read
 // through the caches, where it stays between calls. (A template parameter:
 // a run-time choice inside the load loop doubled the registers.)
-template <int ROWS, class BT, bool STREAM, int CPL>
+// The GEMV's input as stored: row r of A [rows, K].
+struct StoredRows {
+    const float* __restrict__ a;
+    uint64_t k;
+    __device__ __forceinline__ float operator()(int r, uint64_t kk) const { return a[r * k + kk]; }
+};
+
+// `A(r, k)` gives the input's row r at k (StoredRows, or a row normalised in
+// the launch). `prologue()` runs on every thread after the first batch of B
+// rows is in flight (a normalised input's scale; its latency hides under
+// theirs), before any A is read.
+struct NoPrologue {
+    __device__ __forceinline__ void operator()() const {}
+};
+template <int ROWS, class BT, bool STREAM, int CPL, class AF, class PRO = NoPrologue>
 __device__ __forceinline__ void gemv_partial_body(
-    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ partial,
+    const AF& A, const PRO& prologue, const BT* __restrict__ B, float* __restrict__ partial,
     float* __restrict__ C, uint64_t K, uint64_t N, uint64_t k_per_slice, uint32_t cg,
     uint32_t slice, bool direct, const float* __restrict__ addend, int addend_mode) {
     constexpr int H = CPL / 4;  // float4 groups per lane
@@ -863,7 +878,7 @@ __device__ __forceinline__ void gemv_partial_body(
             const float4 b = L::part(raw, h);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                const float a = A[r * K + k];
+                const float a = A(r, k);
                 acc[r][h].x = __builtin_fmaf(a, b.x, acc[r][h].x);
                 acc[r][h].y = __builtin_fmaf(a, b.y, acc[r][h].y);
                 acc[r][h].z = __builtin_fmaf(a, b.z, acc[r][h].z);
@@ -871,13 +886,25 @@ __device__ __forceinline__ void gemv_partial_body(
             }
         }
     };
+    // B rows in flight per lane: 256 bytes for compact weights read 8
+    // columns at a time and for blocks of 8 rows (measured: bf16
+    // 1x4096x11008 22.1 -> 18.3 us, the C1 block 80 -> 61 us), 128 bytes
+    // otherwise (256 was no faster for the f32 decode GEMVs).
+    constexpr int kU = (CPL == 8 || ROWS >= 8 ? 256 : 128) / sizeof(typename L::Raw);
+    uint64_t kk = k_begin + wave;
+    typename L::Raw first[kU];
+    const bool first_batch = live && kk + 4 * (kU - 1) < k_end;
+    if (first_batch) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) first[u] = L::template load<STREAM>(B + (kk + 4 * u) * N + col);
+    }
+    prologue();
     if (live) {
-        // B rows in flight per lane: 256 bytes for compact weights read 8
-        // columns at a time and for blocks of 8 rows (measured: bf16
-        // 1x4096x11008 22.1 -> 18.3 us, the C1 block 80 -> 61 us), 128 bytes
-        // otherwise (256 was no faster for the f32 decode GEMVs).
-        constexpr int kU = (CPL == 8 || ROWS >= 8 ? 256 : 128) / sizeof(typename L::Raw);
-        uint64_t kk = k_begin + wave;
+        if (first_batch) {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) fma_row(first[u], kk + 4 * u);
+            kk += 4 * kU;
+        }
         for (; kk + 4 * (kU - 1) < k_end; kk += 4 * kU) {
             typename L::Raw bv[kU];
 #pragma unroll
@@ -932,8 +959,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     C += rb * ROWS * N;
     if (partial) partial += rb * slices * ROWS * N;
     if (addend_mode == 2) addend += rb * ROWS * N;
-    gemv_partial_body<ROWS, BT, STREAM, CPL>(A, B, partial, C, K, N, k_per_slice, blockIdx.x,
-                                             blockIdx.y, slices == 1, addend, addend_mode);
+    gemv_partial_body<ROWS, BT, STREAM, CPL>(StoredRows{A, K}, NoPrologue{}, B, partial, C, K, N, k_per_slice,
+                                             blockIdx.x, blockIdx.y, slices == 1, addend, addend_mode);
 }
 
 // Sum of the slices' partial sums of 256 columns: wave w adds a fixed
@@ -992,10 +1019,12 @@ __device__ __forceinline__ void gemv_reduce_sum(const float* __restrict__ partia
 }
 
 // C = the slices' partial sums (+ addend).
+// chunk_ss (one row): also the RMSNorm chunk sum of squares of the 256
+// columns written (mhip::chunk_sumsq), at chunk_ss[column group].
 template <int ROWS>
 __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     const float* __restrict__ partial, float* __restrict__ C, uint64_t N, uint32_t slices,
-    const float* __restrict__ addend, int addend_mode) {
+    const float* __restrict__ addend, int addend_mode, float* __restrict__ chunk_ss) {
     const uint64_t rb = blockIdx.z;  // row block, as in gemv_partial_kernel
     partial += rb * slices * ROWS * N;
     C += rb * ROWS * N;
@@ -1005,9 +1034,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     const bool live = col < N;
     float4 v[ROWS];
     gemv_reduce_sum<ROWS>(partial, N, slices, col, live, v);
-    if (wave != 0 || !live) return;
+    if (wave != 0) return;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
+        if (!live) {
+            v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+            continue;
+        }
         if (addend_mode == 1) {
             const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
             v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
@@ -1016,6 +1049,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
             v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
         }
         *reinterpret_cast<float4*>(C + r * N + col) = v[r];
+    }
+    if constexpr (ROWS == 1) {
+        if (chunk_ss) {
+            const float cs = mhip::chunk_sumsq(v[0]);  // dead lanes hold zeros
+            if (lane == 0) chunk_ss[blockIdx.x] = cs;
+        }
     }
 }
 
@@ -1057,19 +1096,60 @@ __device__ __forceinline__ GemvSeg pick(const GemvSet& set, int i) {
     return set.seg[2];
 }
 
-template <int ROWS, class BT, bool STREAM, int CPL>
+// A set's single input row normalised by RMSNorm inside the partial launch
+// (the decode block's FFN RMSNorm): a[k] = src[k] * inv * gain[k], with inv
+// from the row's chunk sums of squares (mhip::chunk_sumsq, written by the
+// launch that produced the row) added in order -- the RMSNorm kernel's bits,
+// for a prologue of `chunks` scalar reads instead of the whole row.
+struct NormIn {
+    const float* src;
+    const float* chunk_ss;
+    const float* gain;
+    float eps;
+    uint32_t chunks;
+};
+
+// Longest k slice a normalised input can have (its LDS staging).
+constexpr uint64_t kNormSliceMax = 4096;
+
+// NORM: 0, rows of A as stored; 1, the single row norm.src normalised.
+template <int ROWS, class BT, bool STREAM, int CPL, int NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const float* __restrict__ A,
-                                                                        uint64_t K, GemvSet set) {
+                                                                        uint64_t K, GemvSet set,
+                                                                        NormIn norm) {
     const uint32_t b = blockIdx.x;
     const int i = (set.count > 2 && b >= set.seg[2].first_block) ? 2
                   : (set.count > 1 && b >= set.seg[1].first_block) ? 1 : 0;
     const GemvSeg s = pick(set, i);
     const uint32_t local = b - s.first_block;
     const uint64_t rb = blockIdx.y;  // row block of ROWS rows
-    gemv_partial_body<ROWS, BT, STREAM, CPL>(A + rb * ROWS * K, static_cast<const BT*>(s.b),
-                                        s.partial + rb * s.slices * ROWS * s.n, nullptr, K, s.n,
-                                        s.k_per_slice, local % s.col_groups, local / s.col_groups,
-                                        false, nullptr, 0);
+    const BT* B = static_cast<const BT*>(s.b);
+    float* partial = s.partial + rb * s.slices * ROWS * s.n;
+    const uint32_t cg = local % s.col_groups, slice = local / s.col_groups;
+    if constexpr (NORM == 0) {
+        gemv_partial_body<ROWS, BT, STREAM, CPL>(StoredRows{A + rb * ROWS * K, K}, NoPrologue{}, B,
+                                                 partial, nullptr, K, s.n, s.k_per_slice, cg, slice,
+                                                 false, nullptr, 0);
+    } else {
+        static_assert(ROWS == 1, "a normalised input is one row");
+        // The workgroup's k slice of the normalised row, staged in LDS once.
+        __shared__ float sa[kNormSliceMax];
+        const uint64_t k0 = static_cast<uint64_t>(slice) * s.k_per_slice;
+        const uint64_t len = min(K, k0 + s.k_per_slice) - k0;
+        auto scale = [&]() {
+            float ss = 0.0f;
+            for (uint32_t c = 0; c < norm.chunks; ++c) ss = ss + norm.chunk_ss[c];
+            const float inv = mhip::inv_rms(ss, K, norm.eps);
+            for (uint64_t j = threadIdx.x; j < len; j += kGemvThreads) {
+                const float y = norm.src[k0 + j] * inv;
+                sa[j] = norm.gain ? y * norm.gain[k0 + j] : y;
+            }
+            __syncthreads();
+        };
+        auto normed = [&](int, uint64_t k) { return sa[k - k0]; };
+        gemv_partial_body<1, BT, STREAM, CPL>(normed, scale, B, partial, nullptr, K, s.n,
+                                              s.k_per_slice, cg, slice, false, nullptr, 0);
+    }
 }
 
 __device__ __forceinline__ float4 rope_vec(const RopeEpi& e, uint64_t row, uint64_t col, float4 v) {
@@ -1175,9 +1255,11 @@ void launch_gemv_partial(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, 
                            static_cast<uint32_t>(slices), addend, mode);
 }
 
+// chunk_ss (one row, split k): the output's RMSNorm chunk sums too.
 template <int ROWS, class BT>
 mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t k,
-                        uint64_t n, const float* addend, int mode, uint64_t row_blocks = 1) {
+                        uint64_t n, const float* addend, int mode, uint64_t row_blocks = 1,
+                        float* chunk_ss = nullptr) {
     const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;  // of the reduction
     uint64_t slices, k_per_slice;
     gemv_slicing(ctx, k, n, &slices, &k_per_slice);
@@ -1208,35 +1290,46 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>,
                        dim3(static_cast<unsigned>(col_groups), 1, static_cast<unsigned>(row_blocks)),
                        dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
-                       static_cast<uint32_t>(slices), addend, mode);
+                       static_cast<uint32_t>(slices), addend, mode, chunk_ss);
     return mhip::check_launch("matmul (decode reduction)");
 }
 
+template <int ROWS, class BT, int CPL, int NORM>
+void launch_gemv_set_partial_n(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, uint64_t k,
+                               const GemvSet& set, const NormIn& norm) {
+    if (stream)
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true, CPL, NORM>), grid,
+                           dim3(kGemvThreads), 0, ctx->stream, a, k, set, norm);
+    else
+        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false, CPL, NORM>), grid,
+                           dim3(kGemvThreads), 0, ctx->stream, a, k, set, norm);
+}
+
+// `norm_mode` (NORM of gemv_set_partial_kernel) is nonzero only for one row.
 template <int ROWS, class BT, int CPL>
 void launch_gemv_set_partial(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, uint64_t k,
-                             const GemvSet& set) {
-    if (stream)
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true, CPL>), grid, dim3(kGemvThreads),
-                           0, ctx->stream, a, k, set);
-    else
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false, CPL>), grid, dim3(kGemvThreads),
-                           0, ctx->stream, a, k, set);
+                             const GemvSet& set, int norm_mode, const NormIn& norm) {
+    if constexpr (ROWS == 1) {
+        if (norm_mode == 1) return launch_gemv_set_partial_n<1, BT, CPL, 1>(ctx, grid, stream, a, k, set, norm);
+    }
+    launch_gemv_set_partial_n<ROWS, BT, CPL, 0>(ctx, grid, stream, a, k, set, norm);
 }
 
 // `wide`: the set's segments were planned with 8 columns per lane.
 template <int ROWS, class BT>
 mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet set, int epilogue,
                             const RopeEpi& rq, const RopeEpi& rk, uint32_t reduce_groups,
-                            bool stream, bool wide, uint32_t row_blocks = 1) {
+                            bool stream, bool wide, int norm_mode, const NormIn& norm,
+                            uint32_t row_blocks = 1) {
     uint32_t blocks = 0;
     for (int i = 0; i < set.count; ++i) blocks += set.seg[i].col_groups * set.seg[i].slices;
     const dim3 grid(blocks, row_blocks);
     if constexpr (kGemvWideable<ROWS, BT>) {
-        if (wide) launch_gemv_set_partial<ROWS, BT, 8>(ctx, grid, stream, a, k, set);
-        else launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set);
+        if (wide) launch_gemv_set_partial<ROWS, BT, 8>(ctx, grid, stream, a, k, set, norm_mode, norm);
+        else launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set, norm_mode, norm);
     } else {
         if (wide) return MHIP_LAYOUT_UNSUPPORTED;
-        launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set);
+        launch_gemv_set_partial<ROWS, BT, 4>(ctx, grid, stream, a, k, set, norm_mode, norm);
     }
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
@@ -1505,17 +1598,18 @@ namespace {
 template <class BT>
 mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                               const GemvSet& set, int epilogue, const RopeEpi& rq,
-                              const RopeEpi& rk, uint32_t g, bool stream, bool wide) {
+                              const RopeEpi& rk, uint32_t g, bool stream, bool wide, int norm_mode,
+                              const NormIn& norm) {
     switch (rows) {
-        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
-        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide);
+        case 1: return launch_gemv_set<1, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, norm_mode, norm);
+        case 2: return launch_gemv_set<2, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
+        case 3: return launch_gemv_set<3, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
+        case 4: return launch_gemv_set<4, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
+        case 5: return launch_gemv_set<5, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
+        case 6: return launch_gemv_set<6, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
+        case 7: return launch_gemv_set<7, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm);
         default:
-            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide,
+            return launch_gemv_set<8, BT>(ctx, a, k, set, epilogue, rq, rk, g, stream, wide, 0, norm,
                                           static_cast<uint32_t>(rows / kGemvMaxRows));
     }
 }
@@ -1524,11 +1618,51 @@ mhip_status dispatch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint
 
 namespace mhip {
 
+mhip_status gemv_chunks_f32(mhip_ctx* ctx, const float* a, const void* b, float* out, uint64_t k,
+                            uint64_t n, const float* addend, int addend_mode, bool bf16_weights,
+                            float* chunk_ss) {
+    MHIP_REQUIRE_CTX(ctx);
+    // The one-row GEMV path of mhip_matmul_f32 with a split k (the chunk
+    // sums come from its reduction launch).
+    const uintptr_t b_align = bf16_weights ? 7u : 15u;
+    if (!a || !b || !out || !chunk_ss || k == 0 || n % 4 != 0 || !aligned16(out) ||
+        (reinterpret_cast<uintptr_t>(b) & b_align) != 0 || (addend_mode != 0 && !addend) ||
+        addend_mode < 0 || addend_mode > 2)
+        return MHIP_LAYOUT_UNSUPPORTED;
+    uint64_t slices, k_per_slice;
+    gemv_slicing(ctx, k, n, &slices, &k_per_slice);
+    if (slices < 2) return MHIP_LAYOUT_UNSUPPORTED;
+    return bf16_weights
+               ? launch_gemv<1, uint16_t>(ctx, a, static_cast<const uint16_t*>(b), out, k, n, addend,
+                                          addend_mode, 1, chunk_ss)
+               : launch_gemv<1, float>(ctx, a, static_cast<const float*>(b), out, k, n, addend,
+                                       addend_mode, 1, chunk_ss);
+}
+
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
                          const GemvTarget* targets, int count, int epilogue,
-                         const mhip_rope_params* rope, bool bf16_weights) {
+                         const mhip_rope_params* rope, bool bf16_weights, const RowNorm* row_norm) {
     MHIP_REQUIRE_CTX(ctx);
-    if (!a || !targets || count < 1 || count > 3 || rows == 0 || k == 0) return MHIP_LAYOUT_UNSUPPORTED;
+    if (!targets || count < 1 || count > 3 || rows == 0 || k == 0) return MHIP_LAYOUT_UNSUPPORTED;
+    if (!row_norm && !a) return MHIP_LAYOUT_UNSUPPORTED;
+    NormIn norm{};
+    int norm_mode = 0;
+    if (row_norm) {
+        // One row that the RMSNorm kernel would normalise with its vector
+        // kernel (k % 4 == 0, at most 16384 floats, 16-byte aligned), so that
+        // the chunk sums carry its order.
+        const RowNorm& rn = *row_norm;
+        int g = 0, vpt = 0;
+        if (rows != 1 || k % 4 != 0 || !rn.src || !rn.chunk_ss || !(rn.eps > 0.0f) ||
+            !aligned16(rn.src) || (rn.gain && !aligned16(rn.gain)) || !rms_layout(k / 4, &g, &vpt))
+            return MHIP_LAYOUT_UNSUPPORTED;
+        norm.src = rn.src;
+        norm.chunk_ss = rn.chunk_ss;
+        norm.gain = rn.gain;
+        norm.eps = rn.eps;
+        norm.chunks = static_cast<uint32_t>((k / 4 + 63) / 64);
+        norm_mode = 1;
+    }
     // Up to 8 rows, or up to 32 in blocks of 8 when every product is small
     // (as for the row-blocked matmul).
     if (rows > kGemvMaxRows) {
@@ -1579,6 +1713,9 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
         if (!(epilogue == kGemvSiluMul && i == 1)) groups += (t.n + kGemvCols - 1) / kGemvCols;
     }
     if (blocks >= (1ULL << 31)) return MHIP_LAYOUT_UNSUPPORTED;
+    if (norm_mode)
+        for (int i = 0; i < count; ++i)
+            if (set.seg[i].k_per_slice > kNormSliceMax) return MHIP_LAYOUT_UNSUPPORTED;
     RopeEpi rq{}, rk{};
     if (epilogue == kGemvRopeQK) {
         for (int i = 0; i < 2; ++i) {
@@ -1610,8 +1747,10 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
     float* partial = static_cast<float*>(scratch);
     for (int i = 0; i < count; ++i) set.seg[i].partial = partial + offsets[i];
     const uint32_t g = static_cast<uint32_t>(groups);
-    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream, wide)
-                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream, wide);
+    return bf16_weights ? dispatch_gemv_set<uint16_t>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream,
+                                                      wide, norm_mode, norm)
+                        : dispatch_gemv_set<float>(ctx, a, rows, k, set, epilogue, rq, rk, g, stream,
+                                                   wide, norm_mode, norm);
 }
 
 }  // namespace mhip

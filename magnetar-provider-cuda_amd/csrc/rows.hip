@@ -14,6 +14,7 @@
 // ascending sums only in summation order.
 #include "common.hpp"
 #include "internal.hpp"
+#include "reduce.hpp"
 
 #include <cmath>
 
@@ -21,38 +22,10 @@ namespace {
 
 constexpr int kThreads = 256;
 
-struct SumOp {
-    __device__ float operator()(float a, float b) const { return a + b; }
-    static constexpr float identity() { return 0.0f; }
-};
-struct MaxOp {
-    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-    static constexpr float identity() { return -INFINITY; }
-};
-
-template <class Op>
-__device__ __forceinline__ float wave_reduce(float v, Op op) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// Reduces over the G threads of this row's group. For G == 256 the four
-// waves meet in `scratch` (4 floats); every thread gets the result. REUSE:
-// the caller reduces through `scratch` again, so the reads of this call must
-// finish before the next call's writes (a second barrier).
-template <int G, class Op, bool REUSE = true>
-__device__ __forceinline__ float group_reduce(float v, Op op, float* scratch) {
-    v = wave_reduce(v, op);
-    if constexpr (G == 256) {
-        const int wave = threadIdx.x / 64;
-        if ((threadIdx.x & 63) == 0) scratch[wave] = v;
-        __syncthreads();
-        v = op(op(scratch[0], scratch[1]), op(scratch[2], scratch[3]));
-        if constexpr (REUSE) __syncthreads();
-    }
-    return v;
-}
+using mhip::group_reduce;
+using mhip::MaxOp;
+using mhip::SumOp;
+using mhip::wave_reduce;
 
 // With `ids` set, row r of the input is row ids[r] of `in` (an embedding
 // table of `vocab` rows) and is also copied to `copy` row r: the embedding
@@ -63,7 +36,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
     uint64_t rows, uint64_t cols, uint64_t weight_row_stride, float eps,
     const float* __restrict__ ids, uint64_t vocab, float* __restrict__ copy, uint32_t* flags) {
 #pragma clang fp contract(off)
-    __shared__ float scratch[4];
+    __shared__ float chunk[4 * VPT];  // G == 256: the row's chunk sums
     constexpr int kRowsPerBlock = kThreads / G;
     const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
     const int lane = threadIdx.x % G;
@@ -86,12 +59,24 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(
         // The gain goes out with the row, not after the reduction.
         if (w4 && live && c < cols4) wv[v] = w4[c];
     }
+    // The sum of squares chunk by chunk (mhip::chunk_sumsq): vector v of a
+    // wave's lanes is chunk v (G = 64), or chunk wave + 4 v (G = 256).
+    if constexpr (G == 64) {
 #pragma unroll
-    for (int v = 0; v < VPT; ++v)
-        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
-    ss = group_reduce<G, SumOp, false>(ss, SumOp{}, scratch);
+        for (int v = 0; v < VPT; ++v) ss = ss + mhip::chunk_sumsq(x[v]);
+    } else {
+        const int wave = threadIdx.x / 64;
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+            const float cs = mhip::chunk_sumsq(x[v]);
+            if ((threadIdx.x & 63) == 0) chunk[wave + 4 * v] = cs;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4 * VPT; ++j) ss = ss + chunk[j];
+    }
     if (!live) return;
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    const float inv = mhip::inv_rms(ss, cols, eps);
     float4* o4 = reinterpret_cast<float4*>(out) + row * cols4;
     float4* c4 = copy ? reinterpret_cast<float4*>(copy) + row * cols4 : nullptr;
 #pragma unroll
@@ -285,15 +270,15 @@ void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weig
 template <RowKind KIND>
 bool dispatch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weight, float* out,
                   uint64_t cols, uint64_t wstride, float eps, const Gather& g = Gather{}) {
-    const uint64_t c4 = cols / 4;
-    if (c4 <= 64) launch_vec<KIND, 64, 1>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 128) launch_vec<KIND, 64, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 256) launch_vec<KIND, 64, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 512) launch_vec<KIND, 256, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 1024) launch_vec<KIND, 256, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 2048) launch_vec<KIND, 256, 8>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else if (c4 <= 4096) launch_vec<KIND, 256, 16>(ctx, rows, in, weight, out, cols, wstride, eps, g);
-    else return false;
+    int gs = 0, vpt = 0;
+    if (!mhip::rms_layout(cols / 4, &gs, &vpt)) return false;
+    if (gs == 64 && vpt == 1) launch_vec<KIND, 64, 1>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (gs == 64 && vpt == 2) launch_vec<KIND, 64, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (gs == 64) launch_vec<KIND, 64, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (vpt == 2) launch_vec<KIND, 256, 2>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (vpt == 4) launch_vec<KIND, 256, 4>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else if (vpt == 8) launch_vec<KIND, 256, 8>(ctx, rows, in, weight, out, cols, wstride, eps, g);
+    else launch_vec<KIND, 256, 16>(ctx, rows, in, weight, out, cols, wstride, eps, g);
     return true;
 }
 

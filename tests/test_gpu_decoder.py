@@ -13,6 +13,18 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-4
 
 
+def poisoned(block):
+    """The block with NaN in every workspace float, so a value read before the
+    block writes it shows up in the output rather than depending on what the
+    allocation held before."""
+    import ctypes
+    from magnetar_hip._lib import call
+    nan = np.full(block.ws.shape, np.nan, np.float32)
+    call("mhip_upload", block.dev.ctx, ctypes.c_void_p(block.ws.ptr), nan.ctypes.data_as(ctypes.c_void_p),
+         nan.nbytes)
+    return block
+
+
 def weights_for(orc, shapes, seed=0):
     w = {}
     for i, (name, shape) in enumerate(shapes.weight_shapes().items()):
@@ -31,7 +43,7 @@ def test_tiny_block_prefill_and_decode(dev, orc):
     from reference_chain import reference_block
     s = Shapes(vocab=1024, hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=688)
     w = weights_for(orc, s, 100)
-    block = DecoderBlock(dev, s, w, cache_rows=64, max_seq=32)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=64, max_seq=32))
     ids = orc.token_ids(32, 7, 1024)
     got = block.forward(dev.upload(ids), 0).numpy()
     dev.check_flags()
@@ -55,7 +67,7 @@ def test_gqa_block(dev, orc):
     s = Shapes(vocab=512, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024, eps=1e-6,
                rope_base=500000.0)
     w = weights_for(orc, s, 200)
-    block = DecoderBlock(dev, s, w, cache_rows=80, max_seq=70)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=80, max_seq=70))
     ids = orc.token_ids(70, 8, 512)
     got = block.forward(dev.upload(ids), 0).numpy()
     want, _, _ = reference_block(orc, s, w, ids, 0, np.zeros((80, 128), np.float32),
@@ -71,7 +83,7 @@ def test_llama2_7b_block_decode_at_kv_2048(dev, orc):
     s = Shapes(vocab=32000, hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     w = weights_for(orc, s, 300)
     rows = 2049
-    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1))
     kc = np.zeros((rows, 4096), np.float32)
     vc = np.zeros((rows, 4096), np.float32)
     kc[:2048] = orc.normal(2048 * 4096, 301, 0.0, 0.5).reshape(2048, 4096)
@@ -142,21 +154,29 @@ def unfused_block(dev, s, w, ids, position, k_cache, v_cache):
     return ops.matmul(dev, f, w["w_down"], addend=x2, addend_mode=2)
 
 
-@pytest.mark.parametrize("seq,position", [(1, 40), (3, 20), (8, 0), (16, 8), (24, 0), (32, 0),
-                                          (20, 4), (40, 0)])
-def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, position):
-    """The decode fusions (embedding + rmsnorm, Q/K/V GEMVs with RoPE in the
+@pytest.mark.parametrize("seq,position,hidden", [(1, 40, 512), (3, 20, 512), (8, 0, 512), (16, 8, 512),
+                                                 (24, 0, 512), (32, 0, 512), (20, 4, 512), (40, 0, 512),
+                                                 (1, 40, 256), (1, 7, 2048), (1, 0, 4096)])
+def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, position, hidden):
+    """The decode fusions (embedding + rmsnorm, or for one token both
+    RMSNorms inside the projections' launches; Q/K/V GEMVs with RoPE in the
     reduction, gate/up GEMVs with silu * up) change launches, not arithmetic:
     the block output and the cache rows equal the unfused chain's bit for bit.
     16-32 rows take the sets in row blocks of 8; 20 and 40 rows take the
-    separate calls in the block too."""
+    separate calls in the block too. Hidden 256/512 normalise a row with one
+    wave, 2048/4096 with a workgroup of four."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
-    s = Shapes(vocab=1024, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1376)
+    head_dim = 64 if hidden <= 512 else 128
+    s = Shapes(vocab=1024, hidden=hidden, heads=hidden // head_dim, kv_heads=2, head_dim=head_dim,
+               ffn=1376)
     w = weights_for(orc, s, 500)
+    for name in ("attn_norm", "ffn_norm"):  # gains other than 1, so their order shows
+        w[name] = 1.0 + 0.1 * orc.normal(hidden, 510 + len(name), 0.0, 1.0)
     rows = 64
-    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=40)
-    kc = orc.normal(rows * 128, 501, 0.0, 0.5).reshape(rows, 128)
-    vc = orc.normal(rows * 128, 502, 0.0, 0.5).reshape(rows, 128)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=rows, max_seq=40))
+    kv = s.kv_heads * s.head_dim
+    kc = orc.normal(rows * kv, 501, 0.0, 0.5).reshape(rows, kv)
+    vc = orc.normal(rows * kv, 502, 0.0, 0.5).reshape(rows, kv)
     block.k_cache = dev.upload(kc)
     block.v_cache = dev.upload(vc)
     k2, v2 = dev.upload(kc), dev.upload(vc)

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from conftest import max_normwise_err
-from test_gpu_decoder import unfused_block, weights_for
+from test_gpu_decoder import poisoned, unfused_block, weights_for
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def test_random_block(dev, orc, seed):
     w = weights_for(orc, s, 900 + 20 * seed)
     rows = position + seq + 3
     kv_dim = kv_heads * head_dim
-    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=seq)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=rows, max_seq=seq))
     kc = orc.normal(rows * kv_dim, 910 + seed, 0.0, 0.5).reshape(rows, kv_dim)
     vc = orc.normal(rows * kv_dim, 920 + seed, 0.0, 0.5).reshape(rows, kv_dim)
     block.k_cache = dev.upload(kc)
