@@ -6,7 +6,7 @@ matmul / rmsnorm / attention, each held to 1e-4, and the elementwise ops)."""
 import numpy as np
 import pytest
 
-from conftest import max_normwise_err
+from conftest import max_normwise_err, max_rel_err_significant
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +94,8 @@ def test_llama2_7b_block_decode_at_kv_2048(dev, orc):
     got = block.forward(dev.upload(tok), 2048).numpy()
     want, _, _ = reference_block(orc, s, w, tok, 2048, kc, vc)
     err = max_normwise_err(got, want)
-    print(f"llama2-7b decode: {err:.2e}")
+    print(f"llama2-7b decode: {err:.2e}, elementwise (|ref| >= 1e-3 max) "
+          f"{max_rel_err_significant(got, want):.2e}")
     assert err <= TOL
 
 
@@ -114,7 +115,8 @@ def test_llama2_7b_block_prefill(dev, orc):
     err = max_normwise_err(got, want)
     k_err = max_normwise_err(block.k_cache.numpy(), kc)
     v_err = max_normwise_err(block.v_cache.numpy(), vc)
-    print(f"llama2-7b prefill(512): out {err:.2e}, K rows {k_err:.2e}, V rows {v_err:.2e}")
+    print(f"llama2-7b prefill(512): out {err:.2e}, K rows {k_err:.2e}, V rows {v_err:.2e}, "
+          f"elementwise out (|ref| >= 1e-3 max) {max_rel_err_significant(got, want):.2e}")
     assert err <= TOL and k_err <= TOL and v_err <= TOL
 
 
