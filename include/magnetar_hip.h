@@ -538,6 +538,17 @@ mhip_kernel_error mhip_executor_replay_step(mhip_executor* ex, const char* id, u
                                             const uint64_t* input_lengths, int input_count);
 mhip_kernel_error mhip_executor_release_step_capture(mhip_executor* ex, const char* id);
 mhip_status mhip_executor_set_sync_nodes(mhip_executor* ex, int enabled);
+/* Deferred device checks (no counterpart in the reference, which reads the
+ * failure flags after every embedding and softmax dispatch,
+ * src/kernels.rs:3946-3968 and :4360; that stays the default). Enabled, those
+ * dispatches return without waiting for the device, and the flags are read
+ * once at the next tensor read, greedy selection, step-capture start,
+ * mhip_executor_check or disable. A failure found there is returned by that
+ * call, in the dispatch's category, naming the first unchecked dispatch; the
+ * failing dispatch's output has been written by then. For executor-driven
+ * chains that should not pay one host round trip per lookup. */
+mhip_kernel_error mhip_executor_set_deferred_checks(mhip_executor* ex, int enabled);
+mhip_kernel_error mhip_executor_check(mhip_executor* ex);
 /* The observation log (last 4096 entries, src/executor.rs:82). */
 uint64_t mhip_executor_observation_count(mhip_executor* ex);
 mhip_status mhip_executor_observation(mhip_executor* ex, uint64_t index, mhip_observation* out);

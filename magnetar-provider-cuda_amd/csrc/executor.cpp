@@ -222,8 +222,42 @@ struct mhip_executor {
     uint64_t next_handle = 1;
     std::deque<Observation> observations;
     bool sync_nodes = false;
+    // Deferred device checks: the failure flags of embedding and softmax are
+    // read at the next materialisation (a tensor read, a greedy selection,
+    // a capture's start or an explicit check) instead of after each dispatch.
+    bool deferred_checks = false;
+    std::string pending_check;  // the first dispatch not yet checked
+    uint64_t pending_count = 0;
 
     static constexpr size_t kObservationCapacity = 4096;
+
+    // The failure-flag check after a dispatch that can raise one: now (the
+    // reference's order, src/kernels.rs:3946-3968 and :4360), or noted for
+    // flush_checks when checks are deferred.
+    void device_check(const Invocation& inv) {
+        if (deferred_checks) {
+            if (pending_count++ == 0)
+                pending_check = "'" + inv.kernel + "' invocation '" + inv.id + "'";
+            return;
+        }
+        mhip_status st = mhip_check_flags(ctx, nullptr);
+        if (st != MHIP_OK) raise(map_status(st), mhip_last_error_detail());
+    }
+
+    // Reads the flags once for every deferred check; a failure names the
+    // first unchecked dispatch and how many share the check.
+    void flush_checks() {
+        if (pending_count == 0) return;
+        const std::string first = pending_check;
+        const uint64_t count = pending_count;
+        pending_check.clear();
+        pending_count = 0;
+        mhip_status st = mhip_check_flags(ctx, nullptr);
+        if (st != MHIP_OK)
+            raise(map_status(st), std::string(mhip_last_error_detail()) +
+                                      " (deferred check of " + std::to_string(count) +
+                                      " dispatch(es) from " + first + ")");
+    }
 
     void observe(int kind, const Invocation& inv, int error = 0) {
         observations.push_back({kind, inv.kernel, inv.id, error});
@@ -342,8 +376,7 @@ struct mhip_executor {
             capture->has_embedding = true;
             capture->embedding_ids[inv.inputs[1].id] = vocab;
         } else {
-            mhip_status st = mhip_check_flags(ctx, nullptr);
-            if (st != MHIP_OK) raise(map_status(st), mhip_last_error_detail());
+            device_check(inv);
         }
         if (factor) check(mhip_scale_f32(ctx, out->f(), out->f(), *factor, num * dim));
         return out;
@@ -511,15 +544,14 @@ struct mhip_executor {
     }
 
     // src/kernels.rs:4357-4386.
-    BufferPtr op_softmax(const Buffer& x, BufferPtr& offered) {
+    BufferPtr op_softmax(const Invocation& inv, const Buffer& x, BufferPtr& offered) {
         // Its failure check reads the device (src/kernels.rs:4360).
         check(mhip::forbid_in_capture(ctx, "softmax"));
         require_f32(x, "softmax");
         auto [rows, cols] = rows_cols(x);
         BufferPtr out = alloc_output(offered, x.shape, MHIP_DTYPE_F32);
         check(mhip_softmax_rows_f32(ctx, x.f(), out->f(), rows, cols));
-        mhip_status st = mhip_check_flags(ctx, nullptr);
-        if (st != MHIP_OK) raise(map_status(st), mhip_last_error_detail());
+        device_check(inv);
         return out;
     }
 
@@ -792,7 +824,7 @@ struct mhip_executor {
         if (name == "rmsnorm") return op_rmsnorm(inv, offered);
         if (name == "rope") return op_rope(inv, offered);
         if (name == "attention") return op_attention(inv, offered);
-        if (name == "softmax") return op_softmax(get(inv, 0), offered);
+        if (name == "softmax") return op_softmax(inv, get(inv, 0), offered);
         if (name == "silu") return op_silu(get(inv, 0), offered);
         if (name == "add") return op_add(get(inv, 0), get(inv, 1), offered);
         if (name == "mul") return op_mul(get(inv, 0), get(inv, 1), offered);
@@ -1188,6 +1220,7 @@ mhip_kernel_error mhip_executor_read_tensor(mhip_executor* ex, const char* id, v
     return guarded([&] {
         if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
         std::lock_guard<std::mutex> lock(ex->mu);
+        ex->flush_checks();
         auto it = ex->storage.find(id);
         if (it == ex->storage.end())
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + id);
@@ -1214,6 +1247,7 @@ mhip_kernel_error mhip_executor_read_tensor_values(mhip_executor* ex, const char
     return guarded([&] {
         if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
         std::lock_guard<std::mutex> lock(ex->mu);
+        ex->flush_checks();
         auto it = ex->storage.find(id);
         if (it == ex->storage.end())
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + id);
@@ -1241,6 +1275,7 @@ mhip_kernel_error mhip_executor_read_tensor_rows(mhip_executor* ex, const char* 
     return guarded([&] {
         if (!ex || !id) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor or id");
         std::lock_guard<std::mutex> lock(ex->mu);
+        ex->flush_checks();
         auto it = ex->storage.find(id);
         if (it == ex->storage.end())
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + id);
@@ -1340,6 +1375,23 @@ mhip_kernel_error mhip_executor_execute(mhip_executor* ex, const mhip_invocation
     return mhip_executor_complete_kernel(ex, handle);
 }
 
+mhip_kernel_error mhip_executor_set_deferred_checks(mhip_executor* ex, int enabled) {
+    return guarded([&] {
+        if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        ex->deferred_checks = enabled != 0;
+        if (!enabled) ex->flush_checks();
+    });
+}
+
+mhip_kernel_error mhip_executor_check(mhip_executor* ex) {
+    return guarded([&] {
+        if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
+        std::lock_guard<std::mutex> lock(ex->mu);
+        ex->flush_checks();
+    });
+}
+
 mhip_status mhip_executor_set_sync_nodes(mhip_executor* ex, int enabled) {
     if (!ex) return MHIP_SHAPE_UNSUPPORTED;
     std::lock_guard<std::mutex> lock(ex->mu);
@@ -1374,6 +1426,7 @@ mhip_kernel_error mhip_executor_select_greedy_column(mhip_executor* ex, const ch
         if (!ex || !logits || !column) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor, id or result");
         *column = -1;
         std::lock_guard<std::mutex> lock(ex->mu);
+        ex->flush_checks();
         auto it = ex->storage.find(logits);
         if (it == ex->storage.end())
             raise(MHIP_KERNEL_EXECUTION_FAILED, std::string("no materialized data for resource ") + logits);
@@ -1397,6 +1450,7 @@ mhip_kernel_error mhip_executor_begin_step_capture(mhip_executor* ex, const char
         if (!ex) raise(MHIP_KERNEL_EXECUTION_FAILED, "null executor");
         std::lock_guard<std::mutex> lock(ex->mu);
         if (ex->capture) raise(MHIP_KERNEL_EXECUTION_FAILED, "a step capture is already in progress");
+        ex->flush_checks();
         uint32_t bits = 0;
         for (int i = 0; i < count; ++i) {
             const std::string name = advancing && advancing[i] ? advancing[i] : "";

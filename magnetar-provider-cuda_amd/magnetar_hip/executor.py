@@ -119,6 +119,8 @@ _SIGS = {
     "mhip_executor_complete_kernel": ([_P, _U64], ctypes.c_int),
     "mhip_executor_execute": ([_P, ctypes.POINTER(_Invocation)], ctypes.c_int),
     "mhip_executor_set_sync_nodes": ([_P, ctypes.c_int], ctypes.c_int),
+    "mhip_executor_set_deferred_checks": ([_P, ctypes.c_int], ctypes.c_int),
+    "mhip_executor_check": ([_P], ctypes.c_int),
     "mhip_executor_observation_count": ([_P], _U64),
     "mhip_executor_observation": ([_P, _U64, ctypes.POINTER(_Observation)], ctypes.c_int),
     "mhip_provider_create": ([ctypes.c_int, ctypes.c_char_p, ctypes.POINTER(_P)], ctypes.c_int),
@@ -366,6 +368,7 @@ class Executor:
         """The greedy column of `logits` row `row` (src/executor.rs:2549-2564), or
         None when no column is eligible or the selection fails, as the
         reference's Option."""
+        self.check()  # a deferred failure raises rather than reading as None
         flat = [int(v) for r in excluded for v in (r[0], r[1])]
         ranges = (ctypes.c_uint64 * max(1, len(flat)))(*flat)
         col = ctypes.c_int64(-1)
@@ -408,6 +411,17 @@ class Executor:
 
     def set_sync_nodes(self, enabled: bool) -> None:
         _lib.check(_lib_bound().mhip_executor_set_sync_nodes(self._h, int(enabled)))
+
+    def set_deferred_checks(self, enabled: bool) -> None:
+        """Enabled, embedding and softmax dispatches no longer wait for their
+        failure flags; the next read, greedy selection, capture start or
+        check() reads them once and raises the deferred failure. Disabling
+        checks what is pending."""
+        _check(_lib_bound().mhip_executor_set_deferred_checks(self._h, int(enabled)))
+
+    def check(self) -> None:
+        """Raises the failure of any dispatch whose check was deferred."""
+        _check(_lib_bound().mhip_executor_check(self._h))
 
     def observations(self):
         lib = _lib_bound()

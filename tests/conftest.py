@@ -77,3 +77,10 @@ def max_rel_err_significant(actual, expected, frac: float = 1e-3) -> float:
     if not keep.any():
         return 0.0
     return float(np.max(np.abs(a[keep] - e[keep]) / np.abs(e[keep])))
+
+
+def sweep_seeds(n: int) -> range:
+    """Seeds of a randomized sweep: n by default, n * MHIP_SWEEP_SCALE when
+    that is set (a wider sweep on demand; every seed is its own case)."""
+    import os
+    return range(n * max(1, int(os.environ.get("MHIP_SWEEP_SCALE", "1"))))

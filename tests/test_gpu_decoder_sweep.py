@@ -6,7 +6,7 @@ normwise."""
 import numpy as np
 import pytest
 
-from conftest import max_normwise_err
+from conftest import max_normwise_err, sweep_seeds
 from test_gpu_decoder import poisoned, unfused_block, weights_for
 
 pytestmark = pytest.mark.gpu
@@ -24,7 +24,7 @@ def draw(seed):
     return head_dim, heads, kv_heads, ffn, vocab, seq, position
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", sweep_seeds(16))
 def test_random_block(dev, orc, seed):
     from magnetar_hip.decoder import DecoderBlock, Shapes
     from reference_chain import reference_block
@@ -33,6 +33,8 @@ def test_random_block(dev, orc, seed):
     s = Shapes(vocab=vocab, hidden=hidden, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
                ffn=ffn)
     w = weights_for(orc, s, 900 + 20 * seed)
+    for i, name in enumerate(("attn_norm", "ffn_norm")):  # gains other than 1
+        w[name] = 1.0 + 0.1 * orc.normal(hidden, 940 + 2 * seed + i, 0.0, 1.0)
     rows = position + seq + 3
     kv_dim = kv_heads * head_dim
     block = poisoned(DecoderBlock(dev, s, w, cache_rows=rows, max_seq=seq))

@@ -357,3 +357,53 @@ def test_out_of_device_memory_is_triggered_by_a_real_over_capacity_allocation(de
     st = _lib.lib().mhip_alloc(dev.ctx, 1024, ctypes.byref(ptr))
     assert st == 0 and ptr.value
     _lib.check(_lib.lib().mhip_free(dev.ctx, ptr))
+
+
+def test_deferred_checks_report_at_the_next_read(ex, orc):
+    """With deferred checks an invalid embedding id or an all -inf softmax row
+    no longer fails its dispatch: the next read (or check()) raises it in the
+    same category, naming the first unchecked dispatch; valid chains give the
+    same bits as with the reference's per-dispatch checks."""
+    from magnetar_hip import KernelError, KernelInvocation, TensorRef
+    table = orc.normal(16 * 8, 71).reshape(16, 8)
+    ex.write_tensor("table", table)
+    ex.write_tensor("ids", np.array([3.0, 15.0, 0.0], np.float32))
+    ex.write_tensor("bad", np.array([2.0, 16.0], np.float32))
+    ex.write_tensor("m", np.full((2, 3), -np.inf, np.float32))
+    ex.execute(inv("embedding", ["table", "ids"], "e"))
+    ex.execute(inv("softmax", ["e"], "p"))
+    eager = ex.read_tensor("p")
+    ex.set_deferred_checks(True)
+    try:
+        ex.execute(inv("embedding", ["table", "ids"], "e2"))
+        ex.execute(inv("softmax", ["e2"], "p2"))
+        assert_bitexact(ex.read_tensor("p2"), eager)
+        ex.execute(KernelInvocation("embedding", [TensorRef("table"), TensorRef("bad")],
+                                    [TensorRef("e3")], {}, id="lookup-7"))
+        ex.execute(inv("softmax", ["e"], "p3"))  # valid, shares the check
+        with pytest.raises(KernelError) as err:
+            ex.read_tensor("p3")
+        assert err.value.code == "KernelShapeUnsupported"
+        assert "valid in-range" in err.value.detail
+        assert "2 dispatch(es)" in err.value.detail and "lookup-7" in err.value.detail
+        assert_bitexact(ex.read_tensor("p3"), eager)  # reported once, then clear
+        ex.execute(inv("softmax", ["m"], "p4"))
+        with pytest.raises(KernelError) as err:
+            ex.check()
+        assert err.value.code == "KernelExecutionFailed"
+        ex.check()
+        ex.execute(inv("softmax", ["m"], "p4"))
+        with pytest.raises(KernelError) as err:
+            ex.select_greedy_column("p3")
+        assert err.value.code == "KernelExecutionFailed"
+        assert ex.select_greedy_column("p3", 1) == int(np.argmax(eager[1]))
+        ex.execute(inv("embedding", ["table", "bad"], "e3"))
+        with pytest.raises(KernelError):  # disabling checks what is pending
+            ex.set_deferred_checks(False)
+    finally:
+        try:
+            ex.set_deferred_checks(False)
+        except KernelError:
+            pass
+    with pytest.raises(KernelError):
+        ex.execute(inv("embedding", ["table", "bad"], "e3"))

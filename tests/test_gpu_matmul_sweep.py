@@ -9,7 +9,7 @@ of the f32 path over the widened weights.
 import numpy as np
 import pytest
 
-from conftest import assert_bitexact, max_normwise_err
+from conftest import assert_bitexact, max_normwise_err, sweep_seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +30,7 @@ def draw(seed):
     return m, k, n, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), int(rng.integers(0, 3))
 
 
-@pytest.mark.parametrize("seed", range(60))
+@pytest.mark.parametrize("seed", sweep_seeds(60))
 def test_random_shape(dev, orc, seed):
     from magnetar_hip import ops
     m, k, n, ta, tb, mode = draw(seed)

@@ -4,7 +4,7 @@ CPU oracle (RMSNorm and softmax within 1e-4 max relative error, RoPE within
 import numpy as np
 import pytest
 
-from conftest import max_rel_err
+from conftest import max_rel_err, sweep_seeds
 from test_gpu_rows import rope_pair_err
 
 pytestmark = pytest.mark.gpu
@@ -16,7 +16,7 @@ def _cols(rng):
                            4 * int(rng.integers(1000, 4200)), int(rng.integers(1, 20000))]))
 
 
-@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("seed", sweep_seeds(30))
 def test_rmsnorm_random(dev, orc, seed):
     from magnetar_hip import ops
     rng = np.random.default_rng(20_000 + seed)
@@ -35,7 +35,7 @@ def test_rmsnorm_random(dev, orc, seed):
     assert err <= 1e-4
 
 
-@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("seed", sweep_seeds(30))
 def test_softmax_random(dev, orc, seed):
     from magnetar_hip import ops
     rng = np.random.default_rng(30_000 + seed)
@@ -50,7 +50,7 @@ def test_softmax_random(dev, orc, seed):
     assert err <= 1e-4
 
 
-@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("seed", sweep_seeds(30))
 def test_rope_random(dev, orc, seed):
     from magnetar_hip import ops
     rng = np.random.default_rng(40_000 + seed)

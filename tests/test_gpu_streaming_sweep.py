@@ -6,7 +6,7 @@ the ragged tails; a 4-byte (f32) or 2-byte (half) offset the unaligned paths.
 import numpy as np
 import pytest
 
-from conftest import assert_bitexact, max_rel_err
+from conftest import assert_bitexact, max_rel_err, sweep_seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -28,7 +28,7 @@ def _draw(seed):
     return n, int(rng.integers(0, 2)), rng
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", sweep_seeds(24))
 def test_f32_streaming_random(dev, orc, seed):
     from magnetar_hip import ops
     n, shift, rng = _draw(seed)
@@ -50,7 +50,7 @@ def test_f32_streaming_random(dev, orc, seed):
     assert_bitexact(ops.bias_add(dev, dm, dev.upload(bias)).numpy(), orc.bias_add(m, bias)[0])
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", sweep_seeds(24))
 def test_half_streaming_random(dev, orc, seed):
     from magnetar_hip import ops, MHIP_F16, MHIP_BF16
     n, shift, _ = _draw(seed)
