@@ -34,6 +34,8 @@
 //  - a generic kernel (any other shape): one wave per (query, head), online
 //    softmax over 64-key chunks.
 #include "common.hpp"
+#include "decode_merge.hpp"
+#include "internal.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -636,83 +638,26 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
 }
 
-// Merges the chunk records of one (batch, head): out = sum_c w_c o_c with
-// w_c = l_c 2^(m_c - M) / sum_c' l_c' 2^(m_c' - M). Thread groups of D4
-// lanes take chunks round-robin; the groups' sums meet in LDS in a fixed
-// order, so every run adds in the same order.
+// Merges the chunk records of one (batch, head) (mhip::merge_decode_chunks,
+// whose fixed order every run repeats) and writes its output row.
 template <int D4>
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     AttnArgs a, uint64_t chunks, const float* __restrict__ part_o,
     const float* __restrict__ part_ml) {
     constexpr int D = 4 * D4;
-    constexpr int kGroups = 256 / D4;
-    __shared__ float rm[4], rt[4];
-    __shared__ float4 red[kGroups][D4];
     const uint64_t bh = blockIdx.x;
     const uint64_t head = bh % a.heads, b = bh / a.heads;
-    const float* ml = part_ml + 2 * bh * chunks;
-    const float* po = part_o + bh * chunks * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-
-    float mx = -INFINITY;
-    for (uint64_t c = threadIdx.x; c < chunks; c += 256) mx = fmaxf(mx, ml[2 * c]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) rm[wave] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3]));
-    float tot = 0.0f;
-    if (M != -INFINITY)
-        for (uint64_t c = threadIdx.x; c < chunks; c += 256) {
-            const float2 e = *reinterpret_cast<const float2*>(ml + 2 * c);
-            if (e.y > 0.0f) tot += e.y * exp2f(e.x - M);
-        }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
-    if (lane == 0) rt[wave] = tot;
-    __syncthreads();
-    const float total = (rt[0] + rt[1]) + (rt[2] + rt[3]);
-
-    const int gi = threadIdx.x / D4, t = threadIdx.x % D4;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (total > 0.0f) {
-        const float inv_total = 1.0f / total;
-        uint64_t c = gi;
-        for (; c + 3 * kGroups < chunks; c += 4 * kGroups) {
-            float4 o[4];
-            float2 e[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                o[u] = *reinterpret_cast<const float4*>(po + (c + u * kGroups) * D + 4 * t);
-                e[u] = *reinterpret_cast<const float2*>(ml + 2 * (c + u * kGroups));
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float w = e[u].y > 0.0f ? e[u].y * exp2f(e[u].x - M) * inv_total : 0.0f;
-                acc.x += w * o[u].x; acc.y += w * o[u].y; acc.z += w * o[u].z; acc.w += w * o[u].w;
-            }
-        }
-        for (; c < chunks; c += kGroups) {
-            const float4 o = *reinterpret_cast<const float4*>(po + c * D + 4 * t);
-            const float2 e = *reinterpret_cast<const float2*>(ml + 2 * c);
-            const float w = e.y > 0.0f ? e.y * exp2f(e.x - M) * inv_total : 0.0f;
-            acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
-        }
-    }
-    red[gi][t] = acc;
-    __syncthreads();
-    if (threadIdx.x >= D4) return;
-    float4 v = red[0][t];
-    for (int g = 1; g < kGroups; ++g) {
-        const float4 r = red[g][t];
-        v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w;
-    }
-    *reinterpret_cast<float4*>(a.out + b * a.o_bs + head * D + 4 * t) = v;
+    const float4 v = mhip::merge_decode_chunks<D4>(part_ml + 2 * bh * chunks, part_o + bh * chunks * D,
+                                                   chunks, 0, D4);
+    if (threadIdx.x < D4)
+        *reinterpret_cast<float4*>(a.out + b * a.o_bs + head * D + 4 * threadIdx.x) = v;
 }
 
+// `keep`: leave the chunk records for the caller's merge (no combine launch)
+// and reserve `keep->extra_bytes` more of the workspace for it.
 template <int D4, int GT>
 mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch,
-                                uint64_t kv_rows, bool bounded) {
+                                uint64_t kv_rows, bool bounded, mhip::DecodeChunks* keep) {
     constexpr int D = 4 * D4;
     constexpr uint64_t kChunk = decode_chunk(D4);
     // The one query (seq == 1) sits at position kv_seq - 1 in every batch
@@ -745,7 +690,9 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
     const uint64_t reserve = bounded ? batch * a.heads * std::max<uint64_t>(1, (kv_rows + kChunk - 1) / kChunk)
                                      : records;
     float* part = nullptr;
-    mhip_status st = attention_workspace(ctx, std::max(records, reserve) * (D + 2) * sizeof(float), &part);
+    const uint64_t record_floats = (std::max(records, reserve) * (D + 2) + 63) / 64 * 64;
+    const size_t extra = keep ? keep->extra_bytes : 0;
+    mhip_status st = attention_workspace(ctx, record_floats * sizeof(float) + extra, &part);
     if (st != MHIP_OK) return st;
     float* part_o = part;
     float* part_ml = part + records * D;
@@ -753,6 +700,13 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
                        dim3(256), 0, ctx->stream, a, lo, chunks, part_o, part_ml);
     st = mhip::check_launch("attention (decode chunks)");
     if (st != MHIP_OK) return st;
+    if (keep) {
+        keep->part_o = part_o;
+        keep->part_ml = part_ml;
+        keep->chunks = chunks;
+        keep->extra = part + record_floats;
+        return MHIP_OK;
+    }
     hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
                        dim3(256), 0, ctx->stream, a, chunks, part_o, part_ml);
     return mhip::check_launch("attention (decode combine)");
@@ -760,12 +714,12 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
 
 template <int D4>
 mhip_status launch_decode(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch, uint64_t kv_rows,
-                          bool bounded) {
+                          bool bounded, mhip::DecodeChunks* keep = nullptr) {
     const uint64_t group = a.heads / a.kv_heads;
-    if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch, kv_rows, bounded);
-    if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch, kv_rows, bounded);
-    if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch, kv_rows, bounded);
-    return launch_decode_group<D4, kMaxGroup>(ctx, a, batch, kv_rows, bounded);
+    if (group == 1) return launch_decode_group<D4, 1>(ctx, a, batch, kv_rows, bounded, keep);
+    if (group == 2) return launch_decode_group<D4, 2>(ctx, a, batch, kv_rows, bounded, keep);
+    if (group <= 4) return launch_decode_group<D4, 4>(ctx, a, batch, kv_rows, bounded, keep);
+    return launch_decode_group<D4, kMaxGroup>(ctx, a, batch, kv_rows, bounded, keep);
 }
 
 // ---------------------------------------------------------------------------
@@ -834,10 +788,14 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, uint64_t 
 
 }  // namespace
 
-extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k,
-                                          const float* v, float* out,
-                                          const mhip_attention_params* p) {
-    MHIP_REQUIRE_CTX(ctx);
+namespace {
+
+// The checks and kernel arguments of mhip_attention_f32; *empty when there
+// is no query row (nothing to do).
+mhip_status prepare_attention(mhip_ctx* ctx, const float* q, const float* k, const float* v,
+                              float* out, const mhip_attention_params* p, AttnArgs* args,
+                              uint64_t* batch_out, bool* empty) {
+    *empty = false;
     if (!p) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention: null params");
     const uint64_t H = p->head_count, Hkv = p->kv_head_count, d = p->head_dimension;
     const uint64_t vd = p->value_dimension ? p->value_dimension : d;
@@ -864,10 +822,14 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
     if (!(p->scale <= 0.0f) && !std::isfinite(p->scale))
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention scale must be finite and positive");
     const uint64_t batch = p->batch ? p->batch : 1;
-    if (p->seq_len == 0) return MHIP_OK;
+    *batch_out = batch;
+    if (p->seq_len == 0) {
+        *empty = true;
+        return MHIP_OK;
+    }
     if (!q || !k || !v || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention: null buffer");
 
-    AttnArgs a;
+    AttnArgs& a = *args;
     a.q = q;
     a.k = k;
     a.v = v;
@@ -896,10 +858,63 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
     a.k_bs = p->kv_batch_stride ? p->kv_batch_stride : p->kv_rows * Hkv * d;
     a.v_bs = p->v_batch_stride ? p->v_batch_stride : p->kv_rows * Hkv * vd;
     a.o_bs = p->out_batch_stride ? p->out_batch_stride : p->seq_len * H * vd;
+    return MHIP_OK;
+}
 
-    const bool aligned = mhip::aligned16(q) && mhip::aligned16(k) && mhip::aligned16(v) &&
-                         mhip::aligned16(out) && a.q_bs % 4 == 0 && a.k_bs % 4 == 0 &&
-                         a.v_bs % 4 == 0 && a.o_bs % 4 == 0;
+bool decode_aligned(const AttnArgs& a) {
+    return mhip::aligned16(a.q) && mhip::aligned16(a.k) && mhip::aligned16(a.v) &&
+           mhip::aligned16(a.out) && a.q_bs % 4 == 0 && a.k_bs % 4 == 0 && a.v_bs % 4 == 0 &&
+           a.o_bs % 4 == 0;
+}
+
+}  // namespace
+
+namespace mhip {
+
+mhip_status attention_decode_chunks_f32(mhip_ctx* ctx, const float* q, const float* k,
+                                        const float* v, const mhip_attention_params* p,
+                                        DecodeChunks* out) {
+    MHIP_REQUIRE_CTX(ctx);
+    if (!out || !p || p->seq_len != 1 || (p->batch && p->batch != 1)) return MHIP_LAYOUT_UNSUPPORTED;
+    AttnArgs a;
+    uint64_t batch = 1;
+    bool empty = false;
+    // No output row is written: the records' consumer merges them. Any
+    // aligned address stands in for the output in the checks.
+    mhip_status st = prepare_attention(ctx, q, k, v, const_cast<float*>(q), p, &a, &batch, &empty);
+    if (st != MHIP_OK) return st;
+    const uint64_t d = a.d;
+    if (empty || !decode_aligned(a) || a.vd != d || d % 4 != 0 || d > 256 || p->kv_seq_len == 0)
+        return MHIP_LAYOUT_UNSUPPORTED;
+    out->heads = a.heads;
+    out->d = d;
+    const bool bounded = p->bounded_key_count != 0;
+    switch (d / 4) {
+        case 1: return launch_decode<1>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 2: return launch_decode<2>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 4: return launch_decode<4>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 8: return launch_decode<8>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 16: return launch_decode<16>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 32: return launch_decode<32>(ctx, a, 1, p->kv_rows, bounded, out);
+        case 64: return launch_decode<64>(ctx, a, 1, p->kv_rows, bounded, out);
+        default: return MHIP_LAYOUT_UNSUPPORTED;
+    }
+}
+
+}  // namespace mhip
+
+extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const float* k,
+                                          const float* v, float* out,
+                                          const mhip_attention_params* p) {
+    MHIP_REQUIRE_CTX(ctx);
+    AttnArgs a;
+    uint64_t batch = 1;
+    bool empty = false;
+    mhip_status pst = prepare_attention(ctx, q, k, v, out, p, &a, &batch, &empty);
+    if (pst != MHIP_OK || empty) return pst;
+    const uint64_t H = a.heads, d = a.d, vd = a.vd;
+
+    const bool aligned = decode_aligned(a);
     if (aligned && p->seq_len == 1 && vd == d && d % 4 == 0 && d <= 256 && p->kv_seq_len > 0) {
         mhip_status st = MHIP_CAPTURE_UNSUPPORTED;
         switch (d / 4) {

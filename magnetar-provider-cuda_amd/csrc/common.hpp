@@ -128,14 +128,18 @@ __device__ __forceinline__ bool valid_embedding_id(float raw, uint64_t vocab, ui
 __device__ __forceinline__ float rope_position(uint64_t offset, uint64_t row, float scale) {
     return static_cast<float>(offset + row) * scale;
 }
-__device__ __forceinline__ void rope_pair_cs(float position, const float* table, uint64_t half,
-                                             uint64_t p, float* cs, float* sn) {
-    const float angle = position * table[p];
-    const float amp = table[half + p];
+// Cosine and sine of one pair at `position` from its frequency and amplitude.
+__device__ __forceinline__ void rope_freq_cs(float position, float freq, float amp, float* cs,
+                                             float* sn) {
+    const float angle = position * freq;
     float s, c;
     sincosf(angle, &s, &c);
     *sn = s * amp;
     *cs = c * amp;
+}
+__device__ __forceinline__ void rope_pair_cs(float position, const float* table, uint64_t half,
+                                             uint64_t p, float* cs, float* sn) {
+    rope_freq_cs(position, table[p], table[half + p], cs, sn);
 }
 __device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float* o1,
                                             float* o2) {

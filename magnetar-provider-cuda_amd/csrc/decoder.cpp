@@ -14,7 +14,8 @@
 // to matmul + add). For decode (up to 8 rows, or up to 32 in blocks of 8 when
 // the products are small) the Q/K/V and gate/up projections each run as one
 // fused GEMV set whose reduction applies RoPE or silu * up, and the embedding
-// row is normalised as it is gathered; every
+// row is normalised as it is gathered; for one token the attention merge and
+// the FFN RMSNorm also ride in the GEMV launches that consume them. Every
 // fusion is bit-identical to the separate calls. All launches go on the
 // context's stream; nothing waits.
 #include <cstring>
@@ -148,18 +149,36 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
     ap.bounded_key_count = 1;
     ap.window_size = -1;
     ap.batch = 1;
-    MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
-    // One token: the O projection's reduction also writes x2's RMSNorm
-    // chunk sums, and the gate/up launch normalises x2 from them (no
-    // RMSNorm launch). Otherwise matmul-residual, then RMSNorm.
-    st = MHIP_LAYOUT_UNSUPPORTED;
-    if (seq == 1)
-        st = mhip::gemv_chunks_f32(ctx, a, w->wo, x2, c.heads * c.head_dim, c.hidden, x, 2, bf16, css);
-    if (st == MHIP_LAYOUT_UNSUPPORTED)
-        MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
-    else if (st != MHIP_OK)
-        return st;
-    const bool have_chunks = st == MHIP_OK && seq == 1;
+    // One token: attention leaves its key-chunk records and the O
+    // projection's partial launch merges them (no merge launch); the O
+    // reduction also writes x2's RMSNorm chunk sums, and the gate/up launch
+    // normalises x2 from them (no RMSNorm launch). Otherwise attention,
+    // matmul-residual and RMSNorm as separate calls.
+    bool have_chunks = false;
+    if (seq == 1) {
+        mhip::DecodeChunks rec;
+        rec.extra_bytes = mhip::gemv_merge_bytes(ctx, c.heads, c.head_dim, c.hidden, w->wo, x2, bf16);
+        st = rec.extra_bytes ? mhip::attention_decode_chunks_f32(ctx, q, k_cache, v_cache, &ap, &rec)
+                             : MHIP_LAYOUT_UNSUPPORTED;
+        if (st == MHIP_OK) {
+            // The records are in flight: no fallback from here on.
+            MHIP_TRY(mhip::gemv_merge_f32(ctx, rec, w->wo, x2, c.hidden, x, 2, bf16, css));
+            have_chunks = true;
+        } else if (st != MHIP_LAYOUT_UNSUPPORTED) {
+            return st;
+        }
+    }
+    if (!have_chunks) {
+        MHIP_TRY(mhip_attention_f32(ctx, q, k_cache, v_cache, a, &ap));
+        st = MHIP_LAYOUT_UNSUPPORTED;
+        if (seq == 1)
+            st = mhip::gemv_chunks_f32(ctx, a, w->wo, x2, c.heads * c.head_dim, c.hidden, x, 2, bf16, css);
+        if (st == MHIP_LAYOUT_UNSUPPORTED)
+            MHIP_TRY(mm(a, w->wo, x2, seq, c.heads * c.head_dim, c.hidden, x, 2));
+        else if (st != MHIP_OK)
+            return st;
+        have_chunks = st == MHIP_OK && seq == 1;
+    }
     // Decode (as for Q/K/V): gate and up as one set of GEMVs whose reduction writes
     // silu(gate) * up. Otherwise two matmuls and silu-mul.
     const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};

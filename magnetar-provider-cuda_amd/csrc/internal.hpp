@@ -76,6 +76,38 @@ mhip_status gemv_chunks_f32(mhip_ctx* ctx, const float* a, const void* b, float*
                             uint64_t n, const float* addend, int addend_mode, bool bf16_weights,
                             float* chunk_ss);
 
+// Single-query decode attention (mhip_attention_f32 with seq_len 1, batch 1)
+// launched without its merge: the key-chunk records are left in the
+// context's workspace for a consumer that merges them itself, followed by
+// `extra_bytes` of workspace for that consumer (`extra`). Returns
+// MHIP_LAYOUT_UNSUPPORTED, with nothing launched, for any call that
+// mhip_attention_f32 would not run on its split-KV decode kernels.
+struct DecodeChunks {
+    size_t extra_bytes = 0;   // in
+    const float* part_o = nullptr;   // [heads][chunks][d]: chunk outputs
+    const float* part_ml = nullptr;  // [heads][chunks][2]: chunk max and weight sum
+    uint64_t chunks = 0, heads = 0, d = 0;
+    float* extra = nullptr;
+};
+mhip_status attention_decode_chunks_f32(mhip_ctx* ctx, const float* q, const float* k,
+                                        const float* v, const mhip_attention_params* p,
+                                        DecodeChunks* out);
+
+// The output projection of one decode token over attention's chunk records:
+// out[n] = merge(records)[k] . b[k, n] (+ addend), k = heads * d, with the
+// merge done inside the GEMV's partial launch (each workgroup merges its k
+// slice of one head) instead of a merge launch. Bit-identical to
+// mhip_attention_f32 followed by gemv_chunks_f32 (whose chunk sums it also
+// writes). gemv_merge_bytes gives the workspace it needs (the records'
+// `extra`), or 0 when the shapes do not fit: a k slice must lie within one
+// head (the GEMV's slice length divides d), the GEMV must split k, and `b`
+// and `out` must be aligned for it.
+size_t gemv_merge_bytes(mhip_ctx* ctx, uint64_t heads, uint64_t d, uint64_t n, const void* b,
+                        const float* out, bool bf16_weights);
+mhip_status gemv_merge_f32(mhip_ctx* ctx, const DecodeChunks& records, const void* b, float* out,
+                           uint64_t n, const float* addend, int addend_mode, bool bf16_weights,
+                           float* chunk_ss);
+
 // While capturing: records that `what` cannot be captured and returns
 // MHIP_CAPTURE_UNSUPPORTED; MHIP_OK otherwise.
 mhip_status forbid_in_capture(mhip_ctx* ctx, const char* what);

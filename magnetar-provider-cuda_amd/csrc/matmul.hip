@@ -41,6 +41,7 @@
 
 #include <mutex>
 #include "internal.hpp"
+#include "decode_merge.hpp"
 #include "reduce.hpp"
 
 namespace {
@@ -963,58 +964,101 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
                                              blockIdx.x, blockIdx.y, slices == 1, addend, addend_mode);
 }
 
-// Sum of the slices' partial sums of 256 columns: wave w adds a fixed
-// quarter of the slices, each row in slice order, then wave 0 adds the
-// quarters in order -- the same order on every run. Loads go out in batches
-// of 16 float4 (all rows of 16 / ROWS slices) before any is added, so a
-// quarter costs ceil(slices / 4 / batch) memory round trips, not one per
-// slice and row. The result is valid in wave 0 only; every thread of the
-// workgroup must call it (it synchronises), and a second call must come
-// after a __syncthreads().
-template <int ROWS>
-__device__ __forceinline__ void gemv_reduce_sum(const float* __restrict__ partial, uint64_t N,
+// A one-row decode GEMV whose input row is attention's output, merged here
+// from its key-chunk records (mhip::merge_decode_chunks, the merge kernel's
+// order) instead of by a merge launch: each workgroup merges its k slice,
+// which lies within one head of D = 4 * D4 columns, into LDS once its first
+// weight rows are in flight.
+template <class BT, bool STREAM, int CPL, int D4>
+__global__ __launch_bounds__(kGemvThreads) void gemv_partial_merge_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml, uint64_t chunks,
+    const BT* __restrict__ B, float* __restrict__ partial, uint64_t K, uint64_t N,
+    uint64_t k_per_slice, uint32_t slices) {
+    static_assert(kGemvThreads == 256, "the merge takes 256 threads");
+    constexpr int D = 4 * D4;
+    __shared__ float sa[D];
+    const uint32_t slice = blockIdx.y;
+    const uint64_t k0 = static_cast<uint64_t>(slice) * k_per_slice;
+    const uint64_t head = k0 / D;
+    const int q0 = static_cast<int>(k0 % D) / 4;
+    const int nq = static_cast<int>(min(K, k0 + k_per_slice) - k0) / 4;
+    auto merge = [&]() {
+        const float4 v = mhip::merge_decode_chunks<D4>(part_ml + 2 * head * chunks,
+                                                       part_o + head * chunks * D, chunks, q0, nq);
+        if (static_cast<int>(threadIdx.x) >= q0 && static_cast<int>(threadIdx.x) < q0 + nq)
+            *reinterpret_cast<float4*>(sa + 4 * (threadIdx.x - q0)) = v;
+        __syncthreads();
+    };
+    auto merged = [&](int, uint64_t k) { return sa[k - k0]; };
+    gemv_partial_body<1, BT, STREAM, CPL>(merged, merge, B, partial, nullptr, K, N, k_per_slice,
+                                          blockIdx.x, slice, slices == 1, nullptr, 0);
+}
+
+// Sums of the slices' partial sums of 256 columns, for NSEG matrices of the
+// same shape at once: wave w adds a fixed quarter of the slices, each row in
+// slice order, then wave 0 adds the quarters in order -- the same order on
+// every run. Loads go out in batches of 16 float4 (every segment's rows of
+// 16 / (ROWS * NSEG) slices) before any is added, so a quarter costs
+// ceil(slices / 4 / batch) memory round trips for all segments together,
+// not one per slice, row or segment. The results are valid in wave 0 only;
+// every thread of the workgroup must call it (it synchronises), and a second
+// call must come after a __syncthreads().
+template <int ROWS, int NSEG = 1>
+__device__ __forceinline__ void gemv_reduce_sum(const float* const (&partial)[NSEG], uint64_t N,
                                                 uint32_t slices, uint64_t col, bool live,
-                                                float4 (&out)[ROWS]) {
+                                                float4 (&out)[NSEG][ROWS]) {
     __shared__ float4 red[4][ROWS][64];
-    constexpr int kBatch = ROWS >= 16 ? 1 : 16 / ROWS;  // slices per batch
+    constexpr int kBatch = ROWS * NSEG >= 16 ? 1 : 16 / (ROWS * NSEG);  // slices per batch
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t quarter = (slices + 3) / 4;
     const uint32_t s_begin = min(slices, wave * quarter), s_end = min(slices, s_begin + quarter);
-    float4 v[ROWS];
+    float4 v[NSEG][ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) v[q][r] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
         for (uint32_t s = s_begin; s < s_end; s += kBatch) {
-            float4 p[kBatch][ROWS];
+            float4 p[NSEG][kBatch][ROWS];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
+            for (int q = 0; q < NSEG; ++q)
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r)
-                    if (s + u < s_end)
-                        p[u][r] = *reinterpret_cast<const float4*>(
-                            partial + ((s + u) * static_cast<uint64_t>(ROWS) + r) * N + col);
+                for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
+                    for (int r = 0; r < ROWS; ++r)
+                        if (s + u < s_end)
+                            p[q][u][r] = *reinterpret_cast<const float4*>(
+                                partial[q] + ((s + u) * static_cast<uint64_t>(ROWS) + r) * N + col);
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r)
-                    if (s + u < s_end) {
-                        v[r].x += p[u][r].x; v[r].y += p[u][r].y; v[r].z += p[u][r].z; v[r].w += p[u][r].w;
-                    }
+            for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+                    for (int r = 0; r < ROWS; ++r)
+                        if (s + u < s_end) {
+                            v[q][r].x += p[q][u][r].x; v[q][r].y += p[q][u][r].y;
+                            v[q][r].z += p[q][u][r].z; v[q][r].w += p[q][u][r].w;
+                        }
         }
     }
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) red[wave][r][lane] = v[r];
-    __syncthreads();
-    if (wave != 0) return;
+    for (int q = 0; q < NSEG; ++q) {
+        if (q > 0) __syncthreads();  // wave 0 has read the previous segment's quarters
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        float4 v = red[0][r][lane];
+        for (int r = 0; r < ROWS; ++r) red[wave][r][lane] = v[q][r];
+        __syncthreads();
+        if (wave == 0) {
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            const float4 o = red[w][r][lane];
-            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+            for (int r = 0; r < ROWS; ++r) {
+                float4 t = red[0][r][lane];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) {
+                    const float4 o = red[w][r][lane];
+                    t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
+                }
+                out[q][r] = t;
+            }
         }
-        out[r] = v;
     }
 }
 
@@ -1032,27 +1076,32 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
     const bool live = col < N;
-    float4 v[ROWS];
-    gemv_reduce_sum<ROWS>(partial, N, slices, col, live, v);
+    // The addend goes out with the partial sums (one memory round trip).
+    float4 add[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        add[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (wave == 0 && live && addend_mode != 0)
+            add[r] = *reinterpret_cast<const float4*>(addend + (addend_mode == 2 ? r * N : 0) + col);
+    }
+    float4 v[1][ROWS];
+    gemv_reduce_sum<ROWS>({partial}, N, slices, col, live, v);
     if (wave != 0) return;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
+        float4& o = v[0][r];
         if (!live) {
-            v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+            o = make_float4(0.f, 0.f, 0.f, 0.f);
             continue;
         }
-        if (addend_mode == 1) {
-            const float4 b4 = *reinterpret_cast<const float4*>(addend + col);
-            v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
-        } else if (addend_mode == 2) {
-            const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + col);
-            v[r].x = v[r].x + b4.x; v[r].y = v[r].y + b4.y; v[r].z = v[r].z + b4.z; v[r].w = v[r].w + b4.w;
+        if (addend_mode != 0) {
+            o.x = o.x + add[r].x; o.y = o.y + add[r].y; o.z = o.z + add[r].z; o.w = o.w + add[r].w;
         }
-        *reinterpret_cast<float4*>(C + r * N + col) = v[r];
+        *reinterpret_cast<float4*>(C + r * N + col) = o;
     }
     if constexpr (ROWS == 1) {
         if (chunk_ss) {
-            const float cs = mhip::chunk_sumsq(v[0]);  // dead lanes hold zeros
+            const float cs = mhip::chunk_sumsq(v[0][0]);  // dead lanes hold zeros
             if (lane == 0) chunk_ss[blockIdx.x] = cs;
         }
     }
@@ -1152,15 +1201,35 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_partial_kernel(const fl
     }
 }
 
-__device__ __forceinline__ float4 rope_vec(const RopeEpi& e, uint64_t row, uint64_t col, float4 v) {
+// The RoPE factors of one lane's 4 columns (two pairs): read before the
+// reduction's partial sums are awaited, so they cost no round trip of their own.
+struct RopeCoef {
+    float f0, a0, f1, a1;  // frequency and amplitude of the two pairs
+    uint64_t offset;
+    bool on;               // the columns lie in the rotated dimensions
+};
+
+__device__ __forceinline__ RopeCoef rope_coef(const RopeEpi& e, uint64_t col) {
+    RopeCoef c{};
     const uint64_t j = col % e.head_width;
-    if (j >= e.dimension) return v;
-    const uint64_t p = j / 2;
-    const uint64_t offset = e.offset + (e.advance ? *e.advance : 0);
-    const float position = mhip::rope_position(offset, row, e.scale);
+    c.on = j < e.dimension;
+    if (c.on) {
+        const uint64_t p = j / 2;
+        c.f0 = e.table[p];
+        c.a0 = e.table[e.half + p];
+        c.f1 = e.table[p + 1];
+        c.a1 = e.table[e.half + p + 1];
+    }
+    c.offset = e.offset + (e.advance ? *e.advance : 0);
+    return c;
+}
+
+__device__ __forceinline__ float4 rope_vec(const RopeCoef& c, float scale, uint64_t row, float4 v) {
+    if (!c.on) return v;
+    const float position = mhip::rope_position(c.offset, row, scale);
     float c0, s0, c1, s1;
-    mhip::rope_pair_cs(position, e.table, e.half, p, &c0, &s0);
-    mhip::rope_pair_cs(position, e.table, e.half, p + 1, &c1, &s1);
+    mhip::rope_freq_cs(position, c.f0, c.a0, &c0, &s0);
+    mhip::rope_freq_cs(position, c.f1, c.a1, &c1, &s1);
     float4 r;
     mhip::rope_rotate(v.x, v.y, c0, s0, &r.x, &r.y);
     mhip::rope_rotate(v.z, v.w, c1, s1, &r.z, &r.w);
@@ -1179,38 +1248,47 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_set_reduce_kernel(GemvSet s
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(b - s.first_group) * kGemvCols + lane * 4;
     const bool live = col < s.n;
-    float4 v[ROWS];
-    gemv_reduce_sum<ROWS>(s.partial + rb * s.slices * ROWS * s.n, s.n, s.slices, col, live, v);
+    float* out = s.out + rb * ROWS * s.n;
     if (epilogue == mhip::kGemvSiluMul) {
-        // Up projection: the same columns of segment 1.
+        // Gate (segment 0) and up (segment 1, the same columns) summed together.
         const GemvSeg u = pick(set, 1);
-        float4 w[ROWS];
-        __syncthreads();
-        gemv_reduce_sum<ROWS>(u.partial + rb * u.slices * ROWS * u.n, u.n, u.slices, col, live, w);
+        const uint64_t advance = (wave == 0 && s.out_advance) ? *s.out_advance : 0;
+        float4 v[2][ROWS];
+        gemv_reduce_sum<ROWS, 2>({s.partial + rb * s.slices * ROWS * s.n,
+                                  u.partial + rb * u.slices * ROWS * u.n},
+                                 s.n, s.slices, col, live, v);
         if (wave != 0 || !live) return;
-        float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0) + rb * ROWS * s.n;
+        out += advance * s.n;
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             float4 o;
-            o.x = mhip::silu1(v[r].x) * w[r].x;
-            o.y = mhip::silu1(v[r].y) * w[r].y;
-            o.z = mhip::silu1(v[r].z) * w[r].z;
-            o.w = mhip::silu1(v[r].w) * w[r].w;
+            o.x = mhip::silu1(v[0][r].x) * v[1][r].x;
+            o.y = mhip::silu1(v[0][r].y) * v[1][r].y;
+            o.z = mhip::silu1(v[0][r].z) * v[1][r].z;
+            o.w = mhip::silu1(v[0][r].w) * v[1][r].w;
             *reinterpret_cast<float4*>(out + r * s.n + col) = o;
         }
         return;
     }
+    const bool rotate = epilogue == mhip::kGemvRopeQK && i < 2;
+    RopeCoef coef{};
+    uint64_t advance = 0;
+    if (wave == 0 && live) {
+        if (rotate) coef = rope_coef(i == 0 ? rope_q : rope_k, col);
+        if (s.out_advance) advance = *s.out_advance;
+    }
+    float4 v[1][ROWS];
+    gemv_reduce_sum<ROWS>({s.partial + rb * s.slices * ROWS * s.n}, s.n, s.slices, col, live, v);
     if (wave != 0 || !live) return;
-    float* out = s.out + (s.out_advance ? *s.out_advance * s.n : 0) + rb * ROWS * s.n;
+    out += advance * s.n;
+    const float scale = i == 0 ? rope_q.scale : rope_k.scale;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        float4 o = v[r];
-        if (epilogue == mhip::kGemvRopeQK && i < 2)
-            o = rope_vec(i == 0 ? rope_q : rope_k, rb * ROWS + r, col, o);
+        float4 o = v[0][r];
+        if (rotate) o = rope_vec(coef, scale, rb * ROWS + r, o);
         *reinterpret_cast<float4*>(out + r * s.n + col) = o;
     }
 }
-
 
 // Whether a GEMV reads its matrix non-temporally: one larger than an XCD's
 // 4 MB L2 is streamed; a smaller one is kept in the caches across calls
@@ -1637,6 +1715,94 @@ mhip_status gemv_chunks_f32(mhip_ctx* ctx, const float* a, const void* b, float*
                                           addend_mode, 1, chunk_ss)
                : launch_gemv<1, float>(ctx, a, static_cast<const float*>(b), out, k, n, addend,
                                        addend_mode, 1, chunk_ss);
+}
+
+size_t gemv_merge_bytes(mhip_ctx* ctx, uint64_t heads, uint64_t d, uint64_t n, const void* b,
+                        const float* out, bool bf16_weights) {
+    const uintptr_t b_align = bf16_weights ? 7u : 15u;
+    if (!ctx || !b || !out || !aligned16(out) || (reinterpret_cast<uintptr_t>(b) & b_align) != 0 ||
+        heads == 0 || n == 0 || n % 4 != 0 || (d != 32 && d != 64 && d != 128 && d != 256))
+        return 0;
+    uint64_t slices, k_per_slice;
+    gemv_slicing(ctx, heads * d, n, &slices, &k_per_slice);
+    if (slices < 2 || k_per_slice > d || d % k_per_slice != 0) return 0;
+    return (slices * n * sizeof(float) + 255) / 256 * 256;
+}
+
+namespace {
+
+template <class BT, int CPL, int D4>
+void launch_merge_partial(mhip_ctx* ctx, dim3 grid, bool stream, const DecodeChunks& r,
+                          const BT* b, float* partial, uint64_t k, uint64_t n, uint64_t k_per_slice,
+                          uint64_t slices) {
+    if (stream)
+        hipLaunchKernelGGL((gemv_partial_merge_kernel<BT, true, CPL, D4>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices));
+    else
+        hipLaunchKernelGGL((gemv_partial_merge_kernel<BT, false, CPL, D4>), grid, dim3(kGemvThreads), 0,
+                           ctx->stream, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
+                           static_cast<uint32_t>(slices));
+}
+
+template <class BT, int CPL>
+void launch_merge_partial_d(mhip_ctx* ctx, dim3 grid, bool stream, const DecodeChunks& r,
+                            const BT* b, float* partial, uint64_t k, uint64_t n,
+                            uint64_t k_per_slice, uint64_t slices) {
+    switch (r.d) {
+        case 32: return launch_merge_partial<BT, CPL, 8>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+        case 64: return launch_merge_partial<BT, CPL, 16>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+        case 128: return launch_merge_partial<BT, CPL, 32>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+        default: return launch_merge_partial<BT, CPL, 64>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+    }
+}
+
+// launch_gemv<1, BT>'s launches (same slicing, column groups, loads and
+// reduction) with the merge kernel's partial launch.
+template <class BT>
+mhip_status launch_gemv_merge(mhip_ctx* ctx, const DecodeChunks& r, const BT* b, float* c,
+                              uint64_t n, const float* addend, int mode, float* chunk_ss) {
+    const uint64_t k = r.heads * r.d;
+    const uint64_t col_groups = (n + kGemvCols - 1) / kGemvCols;
+    uint64_t slices, k_per_slice;
+    gemv_slicing(ctx, k, n, &slices, &k_per_slice);
+    float* partial = r.extra;
+    const bool stream = gemv_streams_b(k * n * sizeof(BT));
+    bool wide = false;
+    if constexpr (kGemvWideable<1, BT>) wide = n % 8 == 0 && mhip::aligned16(b);
+    const uint64_t part_groups = wide ? (n + 511) / 512 : col_groups;
+    const dim3 grid(static_cast<unsigned>(part_groups), static_cast<unsigned>(slices), 1);
+    if constexpr (kGemvWideable<1, BT>) {
+        if (wide)
+            launch_merge_partial_d<BT, 8>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+        else
+            launch_merge_partial_d<BT, 4>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+    } else {
+        launch_merge_partial_d<BT, 4>(ctx, grid, stream, r, b, partial, k, n, k_per_slice, slices);
+    }
+    mhip_status st = mhip::check_launch("attention merge + output projection (partial sums)");
+    if (st != MHIP_OK) return st;
+    hipLaunchKernelGGL(gemv_reduce_kernel<1>, dim3(static_cast<unsigned>(col_groups), 1, 1),
+                       dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
+                       static_cast<uint32_t>(slices), addend, mode, chunk_ss);
+    return mhip::check_launch("attention merge + output projection (reduction)");
+}
+
+}  // namespace
+
+mhip_status gemv_merge_f32(mhip_ctx* ctx, const DecodeChunks& records, const void* b, float* out,
+                           uint64_t n, const float* addend, int addend_mode, bool bf16_weights,
+                           float* chunk_ss) {
+    MHIP_REQUIRE_CTX(ctx);
+    const size_t need = gemv_merge_bytes(ctx, records.heads, records.d, n, b, out, bf16_weights);
+    if (need == 0 || records.extra_bytes < need || !records.extra || !records.part_o ||
+        !records.part_ml || records.chunks == 0 || !chunk_ss || !aligned16(records.extra) ||
+        (addend_mode != 0 && !addend) || addend_mode < 0 || addend_mode > 2)
+        return MHIP_LAYOUT_UNSUPPORTED;
+    return bf16_weights ? launch_gemv_merge<uint16_t>(ctx, records, static_cast<const uint16_t*>(b),
+                                                      out, n, addend, addend_mode, chunk_ss)
+                        : launch_gemv_merge<float>(ctx, records, static_cast<const float*>(b), out,
+                                                   n, addend, addend_mode, chunk_ss);
 }
 
 mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
