@@ -481,8 +481,12 @@ constexpr int kMaxGroup = 8;  // query heads per workgroup; larger groups take s
 // Keys per chunk for head dim 4*D4: kDecodeSteps(D4) steps of 256/D4 keys
 // (D4 lanes hold one key row, 64/D4 keys per wave, four waves). At D >= 16
 // a chunk is 32 KB of K plus 32 KB of V.
+// Calls whose default chunks give every CU 16 workgroups or more (many
+// batch rows or heads, long caches) take twice the steps: half the
+// workgroups and records (C4 decode, B8 KV 4096: 175 -> 171 us).
 __host__ __device__ constexpr int decode_steps(int d4) { return d4 >= 4 ? 8 : 2 * d4; }
-__host__ __device__ constexpr int decode_chunk(int d4) { return decode_steps(d4) * 256 / d4; }
+__host__ __device__ constexpr int decode_chunk(int d4, int steps) { return steps * 256 / d4; }
+__host__ __device__ constexpr int decode_chunk(int d4) { return decode_chunk(d4, decode_steps(d4)); }
 
 // One workgroup per (batch, KV head, key chunk). Every thread issues all of
 // its K and V loads before any arithmetic (2 * kSteps dwordx4 in flight);
@@ -490,14 +494,14 @@ __host__ __device__ constexpr int decode_chunk(int d4) { return decode_steps(d4)
 // the per-wave partial sums meet in LDS. Writes, per query head of the
 // group, the chunk's output normalised by its own weight sum, plus the
 // chunk max (log2 domain) and weight sum.
-template <int D4, int GT>
+template <int D4, int GT, int STEPS>
 __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     AttnArgs a, uint64_t key_base, uint64_t chunks, float* __restrict__ part_o,
     float* __restrict__ part_ml) {
     constexpr int kLPK = D4;              // lanes per key
     constexpr int kKPS = 64 / kLPK;       // keys per wave step
     constexpr int kKPW = 4 * kKPS;        // keys per workgroup step
-    constexpr int kSteps = decode_steps(D4);
+    constexpr int kSteps = STEPS;
     constexpr int D = 4 * D4;
     __shared__ float4 sq[GT][D4];
     __shared__ float4 red[4][GT][D4];
@@ -653,13 +657,53 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
         *reinterpret_cast<float4*>(a.out + b * a.o_bs + head * D + 4 * threadIdx.x) = v;
 }
 
-// `keep`: leave the chunk records for the caller's merge (no combine launch)
-// and reserve `keep->extra_bytes` more of the workspace for it.
+// Keys [lo, hi) in chunks of STEPS steps. `keep`: leave the chunk records
+// for the caller's merge (no combine launch) and reserve `keep->extra_bytes`
+// more of the workspace for it.
+template <int D4, int GT, int STEPS>
+mhip_status launch_decode_chunks(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch, uint64_t kv_rows,
+                                 bool bounded, mhip::DecodeChunks* keep, uint64_t lo, uint64_t hi) {
+    constexpr int D = 4 * D4;
+    constexpr uint64_t kChunk = decode_chunk(D4, STEPS);
+    uint64_t chunks = (hi - lo + kChunk - 1) / kChunk;
+    if (chunks == 0) chunks = 1;
+    const uint64_t slices = (a.heads / a.kv_heads + GT - 1) / GT;
+    const uint64_t units = batch * a.kv_heads * slices;
+    if (units * chunks >= (1ULL << 31))
+        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention decode: too many key chunks");
+    const uint64_t records = batch * a.heads * chunks;
+    // A call bounded by a key count sizes the scratch for every row of K/V
+    // (at the shorter chunks, the most records), so a step captured later at
+    // the same shape never needs to grow it.
+    constexpr uint64_t kShortChunk = decode_chunk(D4);
+    const uint64_t reserve = bounded ? batch * a.heads * std::max<uint64_t>(1, (kv_rows + kShortChunk - 1) / kShortChunk)
+                                     : records;
+    float* part = nullptr;
+    const uint64_t record_floats = (std::max(records, reserve) * (D + 2) + 63) / 64 * 64;
+    const size_t extra = keep ? keep->extra_bytes : 0;
+    mhip_status st = attention_workspace(ctx, record_floats * sizeof(float) + extra, &part);
+    if (st != MHIP_OK) return st;
+    float* part_o = part;
+    float* part_ml = part + records * D;
+    hipLaunchKernelGGL((attn_decode_partial_kernel<D4, GT, STEPS>), dim3(static_cast<unsigned>(units * chunks)),
+                       dim3(256), 0, ctx->stream, a, lo, chunks, part_o, part_ml);
+    st = mhip::check_launch("attention (decode chunks)");
+    if (st != MHIP_OK) return st;
+    if (keep) {
+        keep->part_o = part_o;
+        keep->part_ml = part_ml;
+        keep->chunks = chunks;
+        keep->extra = part + record_floats;
+        return MHIP_OK;
+    }
+    hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
+                       dim3(256), 0, ctx->stream, a, chunks, part_o, part_ml);
+    return mhip::check_launch("attention (decode combine)");
+}
+
 template <int D4, int GT>
 mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch,
                                 uint64_t kv_rows, bool bounded, mhip::DecodeChunks* keep) {
-    constexpr int D = 4 * D4;
-    constexpr uint64_t kChunk = decode_chunk(D4);
     // The one query (seq == 1) sits at position kv_seq - 1 in every batch
     // row and head, so the admitted key range is the same for all of them.
     // A captured call whose key count advances covers every row of K/V; its
@@ -678,38 +722,18 @@ mhip_status launch_decode_group(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch
         lo = lower;
         hi = upper;
     }
-    uint64_t chunks = (hi - lo + kChunk - 1) / kChunk;
-    if (chunks == 0) chunks = 1;
-    const uint64_t slices = (a.heads / a.kv_heads + GT - 1) / GT;
-    const uint64_t units = batch * a.kv_heads * slices;
-    if (units * chunks >= (1ULL << 31))
-        return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention decode: too many key chunks");
-    const uint64_t records = batch * a.heads * chunks;
-    // A call bounded by a key count sizes the scratch for every row of K/V,
-    // so a step captured later at the same shape never needs to grow it.
-    const uint64_t reserve = bounded ? batch * a.heads * std::max<uint64_t>(1, (kv_rows + kChunk - 1) / kChunk)
-                                     : records;
-    float* part = nullptr;
-    const uint64_t record_floats = (std::max(records, reserve) * (D + 2) + 63) / 64 * 64;
-    const size_t extra = keep ? keep->extra_bytes : 0;
-    mhip_status st = attention_workspace(ctx, record_floats * sizeof(float) + extra, &part);
-    if (st != MHIP_OK) return st;
-    float* part_o = part;
-    float* part_ml = part + records * D;
-    hipLaunchKernelGGL((attn_decode_partial_kernel<D4, GT>), dim3(static_cast<unsigned>(units * chunks)),
-                       dim3(256), 0, ctx->stream, a, lo, chunks, part_o, part_ml);
-    st = mhip::check_launch("attention (decode chunks)");
-    if (st != MHIP_OK) return st;
-    if (keep) {
-        keep->part_o = part_o;
-        keep->part_ml = part_ml;
-        keep->chunks = chunks;
-        keep->extra = part + record_floats;
-        return MHIP_OK;
+    constexpr int kSteps = decode_steps(D4);
+    if constexpr (D4 >= 4 && GT <= 2) {
+        // The choice follows the capacity for a bounded call, so its eager
+        // run and a capture of it take the same chunks.
+        const uint64_t span = bounded ? kv_rows : hi - lo;
+        const uint64_t slices = (a.heads / a.kv_heads + GT - 1) / GT;
+        const uint64_t wgs = batch * a.kv_heads * slices * ((span + decode_chunk(D4) - 1) / decode_chunk(D4));
+        const uint64_t cus = ctx->compute_units ? ctx->compute_units : 256;
+        if (wgs >= 16 * cus)
+            return launch_decode_chunks<D4, GT, 2 * kSteps>(ctx, a, batch, kv_rows, bounded, keep, lo, hi);
     }
-    hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
-                       dim3(256), 0, ctx->stream, a, chunks, part_o, part_ml);
-    return mhip::check_launch("attention (decode combine)");
+    return launch_decode_chunks<D4, GT, kSteps>(ctx, a, batch, kv_rows, bounded, keep, lo, hi);
 }
 
 template <int D4>

@@ -197,6 +197,9 @@ DECODE_CASES = [
     (32, 2, 128, 300, 512, (0, 1, 37, 100, 180, 211)),
     (16, 1, 64, 260, 640, (0, 5, 120, 379)),
     (12, 1, 128, 257, 400, (0, 64, 142)),
+    # A store large enough for the double-length key chunks (chosen from the
+    # capacity, so the eager steps and the capture split the keys alike).
+    (32, 32, 128, 2000, 8200, (0, 7, 900)),
 ]
 
 

@@ -40,13 +40,18 @@ def test_kv_write_unaligned_rows_bitexact(dev, orc):
     assert np.array_equal(store.numpy().view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("case,history,heads,kv_heads,dim", [
-    (0, 300, 14, 2, 64),    # grouped decode, seven query heads per KV head
-    (1, 12500, 2, 1, 4),    # a long history of narrow heads
+@pytest.mark.parametrize("case,history,heads,kv_heads,dim,capacity", [
+    (0, 300, 14, 2, 64, 307),      # grouped decode, seven query heads per KV head
+    (1, 12500, 2, 1, 4, 12507),    # a long history of narrow heads
+    # Stores large enough for the decode's double-length key chunks (chosen
+    # from the capacity when the key count is bounded), one and two query
+    # heads per KV head.
+    (2, 3000, 32, 32, 128, 8200),
+    (3, 5000, 32, 16, 128, 16400),
 ])
-def test_key_count_attention_ignores_the_store_tail(dev, orc, case, history, heads, kv_heads, dim):
+def test_key_count_attention_ignores_the_store_tail(dev, orc, case, history, heads, kv_heads, dim,
+                                                    capacity):
     from magnetar_hip import ops
-    capacity = history + 7
     width = kv_heads * dim
     q = orc.attention_values(heads * dim, 10 * case + 1).reshape(1, heads * dim)
     k = orc.attention_values(history * width, 10 * case + 2).reshape(history, width)
