@@ -158,15 +158,17 @@ def unfused_block(dev, s, w, ids, position, k_cache, v_cache):
 
 @pytest.mark.parametrize("seq,position,hidden", [(1, 40, 512), (3, 20, 512), (8, 0, 512), (16, 8, 512),
                                                  (24, 0, 512), (32, 0, 512), (20, 4, 512), (40, 0, 512),
-                                                 (1, 40, 256), (1, 7, 2048), (1, 0, 4096)])
+                                                 (1, 40, 256), (1, 7, 2048), (1, 0, 4096),
+                                                 (4, 3, 2048), (8, 0, 4096), (16, 5, 2048)])
 def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, position, hidden):
-    """The decode fusions (embedding + rmsnorm, or for one token both
-    RMSNorms inside the projections' launches; Q/K/V GEMVs with RoPE in the
-    reduction, gate/up GEMVs with silu * up) change launches, not arithmetic:
-    the block output and the cache rows equal the unfused chain's bit for bit.
-    16-32 rows take the sets in row blocks of 8; 20 and 40 rows take the
-    separate calls in the block too. Hidden 256/512 normalise a row with one
-    wave, 2048/4096 with a workgroup of four."""
+    """The decode fusions (embedding + rmsnorm; for one token the attention
+    merge inside the O projection's launch and the FFN RMSNorm inside the
+    gate/up launch; Q/K/V GEMVs with RoPE in the reduction, gate/up GEMVs with
+    silu * up) change launches, not arithmetic: the block output and the
+    cache rows equal the unfused chain's bit for bit. 16-32 rows take the sets
+    in row blocks of 8; 20 and 40 rows take the separate calls in the block
+    too. Hidden 256/512 normalise a row with one wave, 2048/4096 with a
+    workgroup of four."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
     head_dim = 64 if hidden <= 512 else 128
     s = Shapes(vocab=1024, hidden=hidden, heads=hidden // head_dim, kv_heads=2, head_dim=head_dim,
