@@ -75,6 +75,38 @@ def test_gqa_block(dev, orc):
     assert max_normwise_err(got, want) <= TOL
 
 
+def test_decode_over_more_than_256_key_chunks(dev, orc):
+    """One token against a 33,000-row cache: the attention leaves 258 key
+    chunks per head, more than the merge's 256 threads take in one stride,
+    and the O projection's launch merges them (its k slices of 32 lie inside
+    64-wide heads). Bit-identical to the separate calls, within 1e-4 of the
+    oracle's block."""
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from reference_chain import reference_block
+    s = Shapes(vocab=256, hidden=128, heads=2, kv_heads=2, head_dim=64, ffn=256)
+    w = weights_for(orc, s, 700)
+    for i, name in enumerate(("attn_norm", "ffn_norm")):
+        w[name] = 1.0 + 0.1 * orc.normal(128, 710 + i, 0.0, 1.0)
+    position = 33000
+    rows = position + 1
+    kc = np.zeros((rows, 128), np.float32)
+    vc = np.zeros((rows, 128), np.float32)
+    kc[:position] = orc.normal(position * 128, 701, 0.0, 0.5).reshape(position, 128)
+    vc[:position] = orc.normal(position * 128, 702, 0.0, 0.5).reshape(position, 128)
+    block = poisoned(DecoderBlock(dev, s, w, cache_rows=rows, max_seq=1))
+    block.k_cache = dev.upload(kc)
+    block.v_cache = dev.upload(vc)
+    k2, v2 = dev.upload(kc), dev.upload(vc)
+    tok = orc.token_ids(1, 703, 256)
+    ids = dev.upload(tok)
+    got = block.forward(ids, position).numpy()
+    sep = unfused_block(dev, s, block.w, ids, position, k2, v2).numpy()
+    dev.check_flags()
+    assert np.array_equal(got.view(np.uint32), sep.view(np.uint32))
+    want, _, _ = reference_block(orc, s, w, tok, position, kc, vc)
+    assert max_normwise_err(got, want) <= TOL
+
+
 def test_llama2_7b_block_decode_at_kv_2048(dev, orc):
     """Config 4 decode: hidden 4096, 32 x 128 heads, FFN 11008, one token at
     position 2048 against 2048 cached K/V rows."""
