@@ -80,7 +80,7 @@ mhip_status workspace(mhip_ctx* ctx, size_t bytes, float** out) {
 // KG: the waves form KG groups that each cover the whole tile over every
 // KG-th part of each slice's k (summed in LDS at the end), so a small tile
 // still gives each SIMD two waves.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, int KG = 1>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, int KG = 1, int STEP = 0>
 struct TileCfg {
     static constexpr int kWavesN = BN / WN;
     static constexpr int kTileWaves = (BM / WM) * kWavesN;
@@ -97,8 +97,10 @@ struct TileCfg {
     // Tiles of at most 64 x 64 give a wave only 8 MFMAs per slice, too few
     // to cover a barrier and the first LDS reads of each slice: they move in
     // steps of kGroup slices (one barrier per step), double-buffered, so
-    // kStages = 2 * kGroup slice buffers per operand.
-    static constexpr int kGroup = BM * BN <= 64 * 64 ? 4 : 1;
+    // kStages = 2 * kGroup slice buffers per operand. STEP > 0 sets kGroup
+    // (launch_mfma picks 2 for 8-wave 128 x 128 tiles in a single wave of
+    // workgroups).
+    static constexpr int kGroup = STEP > 0 ? STEP : (BM * BN <= 64 * 64 ? 4 : 1);
     static constexpr int kStages = 2 * kGroup;
     static constexpr int kLdsFloats = kStages * (kLdsA + kLdsB);
     // Global slices as (rows x cols) with cols contiguous in memory.
@@ -258,14 +260,15 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
 // written to out[(row - out_r0) * ldo + (col - out_c0)] for the rows < M and
 // columns < N, plus the addend when addend_mode is 1 or 2. LDS (`lds`) is
 // free on entry and again on return.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG = 1>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG = 1,
+          int STEP = 0>
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT* __restrict__ B,
                                           uint64_t M, uint64_t K, uint64_t N, uint64_t m0,
                                           uint64_t n0, uint64_t k_begin, uint64_t k_end,
                                           float* lds, float* __restrict__ out, uint64_t out_r0,
                                           uint64_t out_c0, uint64_t ldo,
                                           const float* __restrict__ addend, int addend_mode) {
-    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>;
+    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>;
     constexpr int T = Cfg::kThreads;
     // A rows along m (not A_T) and B rows along n (B_T) are swizzled.
     constexpr bool kASwz = !A_T, kBSwz = B_T;
@@ -490,8 +493,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
 // [y * k_split, min(K, (y + 1) * k_split)) and, with more than one split,
 // writes that partial product to C + y * M * N (no addend) for
 // splitk_reduce_kernel.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG>
-__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThreads), 2) void mfma_gemm_kernel(
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG, int STEP>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>::kThreads), 2) void mfma_gemm_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
     uint64_t K, uint64_t N, const float* __restrict__ addend, int addend_mode, uint64_t k_split) {
     extern __shared__ float lds[];
@@ -502,7 +505,7 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThread
     const uint64_t k_end = min(K, k_begin + k_split);
     const bool split = gridDim.y > 1;
     float* out = split ? C + static_cast<uint64_t>(blockIdx.y) * M * N : C;
-    gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG>(
+    gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP>(
         A, B, M, K, N, static_cast<uint64_t>(tm) * BM, static_cast<uint64_t>(tn) * BN, k_begin,
         k_end, lds, out, 0, 0, N, addend, split ? 0 : addend_mode);
 }
@@ -513,8 +516,8 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThread
 // Workgroup w covers units [w * per, (w + 1) * per); per <= slices per tile,
 // so that run touches at most two tiles, and the part of the j-th one goes to
 // slot 2w + j as a BM x BN tile for stream_reduce_kernel.
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG>
-__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThreads), 2) void mfma_gemm_stream_kernel(
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG, int STEP>
+__global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>::kThreads), 2) void mfma_gemm_stream_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ slots, uint64_t M,
     uint64_t K, uint64_t N, uint64_t per) {
     extern __shared__ float lds[];
@@ -528,9 +531,9 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>::kThread
         const uint64_t s1 = min(kslices, s0 + (end - u));
         const uint64_t m0 = t / tiles_n * BM, n0 = t % tiles_n * BN;
         float* slot = slots + (2 * static_cast<uint64_t>(blockIdx.x) + seg) * (BM * BN);
-        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG>(A, B, M, K, N, m0, n0, s0 * BK,
-                                                         min(K, s1 * BK), lds, slot, m0, n0, BN,
-                                                         nullptr, 0);
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP>(A, B, M, K, N, m0, n0, s0 * BK,
+                                                               min(K, s1 * BK), lds, slot, m0, n0,
+                                                               BN, nullptr, 0);
         u += s1 - s0;
     }
 }
@@ -719,21 +722,32 @@ constexpr uint64_t plan_per_cu() {
     return Cfg::kWaves >= 8 ? 1 : std::max<uint64_t>(1, (160u * 1024u) / (Cfg::kLdsFloats * sizeof(float)));
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT, int KG = 1>
+template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, class BT, int KG = 1,
+          int STEP = 0>
 mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
                         uint64_t k, uint64_t n, const float* addend, int mode, bool vec) {
-    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG>;
+    using Cfg = TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>;
     const uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (tiles >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: too many tiles");
     const uint64_t slots = plan_per_cu<Cfg>() * (ctx->compute_units ? ctx->compute_units : 256);
     const GemmPlan plan = plan_gemm(m, k, n, BM, BN, BK, slots);
+    // 8-wave 128 x 128 tiles whose workgroups all fit in one wave on the CUs
+    // take the stepped pipeline (two slices per barrier; 128 KB of LDS, which
+    // leaves no room for a second workgroup, so only then): 2048^3 143 ->
+    // 139 us, 512 x 4096 x 4096 148 -> 145 us; at 3072^3 (nine workgroups per
+    // CU in turn) it was 488 -> 515 us. The same bits either way.
+    if constexpr (STEP == 0 && BM * BN == 128 * 128 && Cfg::kWaves >= 8) {
+        const uint64_t wgs = plan.stream ? plan.groups : tiles * plan.splits;
+        if (wgs <= (ctx->compute_units ? ctx->compute_units : 256))
+            return launch_mfma<BM, BN, BK, WM, WN, A_T, B_T, BT, KG, 2>(ctx, a, b, c, m, k, n, addend, mode, vec);
+    }
     const size_t lds = Cfg::kLdsFloats * sizeof(float);
     static bool configured = false;  // raise the dynamic-LDS cap above 64 KiB once
     if (!configured) {
-        for (const void* f : {reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>),
-                              reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>),
-                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>),
-                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>)})
+        for (const void* f : {reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>),
+                              reinterpret_cast<const void*>(&mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>),
+                              reinterpret_cast<const void*>(&mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>)})
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
@@ -748,10 +762,10 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
         if (st != MHIP_OK) return st;
         const dim3 grid(static_cast<unsigned>(plan.groups));
         if (vec)
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>), grid,
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>), grid,
                                dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
         else
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>), grid,
+            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>), grid,
                                dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
         st = mhip::check_launch("matmul (MFMA stream-K)");
         if (st != MHIP_OK) return st;
@@ -768,11 +782,11 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(plan.splits));
     if (vec)
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, plan.k_split);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG>), grid,
+        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>), grid,
                            dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
                            mode, plan.k_split);
     mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
