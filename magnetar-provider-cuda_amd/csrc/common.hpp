@@ -50,6 +50,7 @@ struct mhip_ctx {
     uint32_t advancing = 0;
     uint64_t* capture_offset = nullptr;
     uint64_t max_offset = 0;
+    bool offset_read = false;  // a captured launch reads the offset word
     std::string capture_failure;
     std::vector<void*> deferred_frees;  // mhip_free calls made while capturing
     // Graphs alive on this context; while any is, buffers it may read (the

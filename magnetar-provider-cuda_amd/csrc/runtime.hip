@@ -55,6 +55,7 @@ uint32_t capture_advancing(const mhip_ctx* ctx) {
 const uint64_t* advance_ptr(mhip_ctx* ctx, uint32_t bit, uint64_t max_offset) {
     if (!ctx->capturing || !(ctx->advancing & bit)) return nullptr;
     if (max_offset < ctx->max_offset) ctx->max_offset = max_offset;
+    ctx->offset_read = true;
     return ctx->capture_offset;
 }
 
@@ -95,6 +96,7 @@ struct mhip_graph {
     hipGraphExec_t exec = nullptr;
     uint64_t* offset = nullptr;
     uint64_t max_offset = 0;
+    bool offset_read = false;  // some launch of the step reads `offset`
 };
 
 namespace {
@@ -357,6 +359,7 @@ mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing) {
     ctx->advancing = advancing;
     ctx->capture_offset = offset;
     ctx->max_offset = UINT64_MAX;
+    ctx->offset_read = false;
     ctx->capture_failure.clear();
     return MHIP_OK;
 }
@@ -399,6 +402,7 @@ mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offs
     g->exec = exec;
     g->offset = ctx->capture_offset;
     g->max_offset = ctx->max_offset;
+    g->offset_read = ctx->offset_read;
     ctx->capture_offset = nullptr;
     ctx->live_graphs += 1;
     *out = g;
@@ -428,10 +432,14 @@ mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset) {
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
                           "offset " + std::to_string(offset) + " leaves the captured bounds (at most " +
                               std::to_string(graph->max_offset) + ")");
-    // The offset is written by a kernel on the same stream, ahead of the graph.
-    hipLaunchKernelGGL(replay_offset_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
-    mhip_status st = mhip::check_launch("writing the replay offset");
-    if (st != MHIP_OK) return st;
+    // The offset is written by a kernel on the same stream, ahead of the
+    // graph; a step none of whose launches advances (nothing reads the word)
+    // replays without it (C1 block graph 59.6 -> 53 us).
+    if (graph->offset_read) {
+        hipLaunchKernelGGL(replay_offset_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
+        mhip_status st = mhip::check_launch("writing the replay offset");
+        if (st != MHIP_OK) return st;
+    }
     return mhip::from_hip(hipGraphLaunch(graph->exec, ctx->stream), "launching a captured step");
 }
 
