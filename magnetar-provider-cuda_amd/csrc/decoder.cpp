@@ -180,7 +180,8 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
         have_chunks = st == MHIP_OK && seq == 1;
     }
     // Decode (as for Q/K/V): gate and up as one set of GEMVs whose reduction writes
-    // silu(gate) * up. Otherwise two matmuls and silu-mul.
+    // silu(gate) * up. Otherwise the gate matmul, then the up matmul with
+    // silu(gate) applied to each finished sum.
     const mhip::GemvTarget gate_up[2] = {{w->w_gate, c.ffn, g}, {w->w_up, c.ffn, nullptr}};
     st = MHIP_LAYOUT_UNSUPPORTED;
     if (have_chunks) {
@@ -198,9 +199,11 @@ mhip_status mhip_block_forward(mhip_ctx* ctx, const mhip_block_config* cfg,
         st = mhip::gemv_set_f32(ctx, h2, seq, c.hidden, gate_up, 2, mhip::kGemvSiluMul, nullptr, bf16);
     }
     if (st == MHIP_LAYOUT_UNSUPPORTED) {
-        MHIP_TRY(mm(h2, w->w_gate, g, seq, c.hidden, c.ffn, nullptr, 0));
-        MHIP_TRY(mm(h2, w->w_up, u, seq, c.hidden, c.ffn, nullptr, 0));
-        MHIP_TRY(mhip_silu_mul_f32(ctx, g, u, g, seq * c.ffn));
+        // The gate product, then the up product gated by it as it is
+        // stored (the bits of the two products and silu-mul).
+        MHIP_TRY(mm(h2, w->w_gate, u, seq, c.hidden, c.ffn, nullptr, 0));
+        MHIP_TRY(mhip::matmul_gated_f32(ctx, h2, w->w_up, bf16, g, seq, c.hidden, c.ffn, false,
+                                        false, u));
     } else if (st != MHIP_OK) {
         return st;
     }

@@ -228,6 +228,12 @@ struct mhip_executor {
     bool deferred_checks = false;
     std::string pending_check;  // the first dispatch not yet checked
     uint64_t pending_count = 0;
+    // The gate product of gated-matmul's matmul path, reused by every call
+    // (stream order makes that safe) and grown when a call needs more; an
+    // outgrown buffer that a captured step may still use stays allocated
+    // until the executor is destroyed.
+    BufferPtr gate_product;
+    std::vector<BufferPtr> retired_gate_products;
 
     static constexpr size_t kObservationCapacity = 4096;
 
@@ -639,13 +645,25 @@ struct mhip_executor {
             if (st != MHIP_LAYOUT_UNSUPPORTED) check(st);
             offered = std::move(out);  // reused below
         }
-        Buffer g(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
-        Buffer u(ctx, m * n * 4, Shape{m, n}, MHIP_DTYPE_F32);
-        check(matmul(a, gate, g.f(), m, k, n, ta, tb, nullptr, 0));
-        check(matmul(a, up, u.f(), m, k, n, ta, tb, nullptr, 0));
+        // The gate product, then the up product with silu(gate) applied to
+        // each finished sum as it is stored.
+        const size_t bytes = std::max<size_t>(m * n * 4, 4);
+        if (!gate_product || gate_product->bytes < bytes) {
+            BufferPtr grown = std::make_unique<Buffer>(ctx, bytes, Shape{m, n}, MHIP_DTYPE_F32);
+            if (gate_product) {
+                if (captures.empty()) {
+                    check(mhip_sync(ctx));  // earlier calls may still use it
+                    gate_product.reset();
+                } else {
+                    retired_gate_products.push_back(std::move(gate_product));
+                }
+            }
+            gate_product = std::move(grown);
+        }
         BufferPtr out = alloc_output(offered, Shape{m, n}, MHIP_DTYPE_F32);
-        check(mhip_silu_mul_f32(ctx, g.f(), u.f(), out->f(), m * n));
-        check(mhip_sync(ctx));  // the temporaries are freed on return
+        check(matmul(a, gate, gate_product->f(), m, k, n, ta, tb, nullptr, 0));
+        check(mhip::matmul_gated_f32(ctx, a.f(), up.ptr, up.compact, out->f(), m, k, n, ta, tb,
+                                     gate_product->f()));
         return out;
     }
 
@@ -1078,6 +1096,8 @@ mhip_status mhip_executor_destroy(mhip_executor* ex) {
         ex->captures.clear();
         mhip_sync(ex->ctx);
         ex->storage.clear();
+        ex->gate_product.reset();
+        ex->retired_gate_products.clear();
     }
     delete ex;
     return MHIP_OK;

@@ -66,6 +66,14 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
                          const mhip_rope_params* rope, bool bf16_weights = false,
                          const RowNorm* norm = nullptr);
 
+// out[m, n] = silu(gate) * (a . b): mhip_matmul_f32 (or the compact-weight
+// matmul, `bf16`) with the gate applied to each finished sum, equal to the
+// product followed by mhip_silu_mul_f32(gate, product) bit for bit. gate is
+// [m, n] (the gate product); out must not overlap it.
+mhip_status matmul_gated_f32(mhip_ctx* ctx, const float* a, const void* b, bool bf16, float* out,
+                             uint64_t m, uint64_t k, uint64_t n, bool transpose_a,
+                             bool transpose_b, const float* gate);
+
 // out[1, n] = a[1, k] . b[k, n] (+ addend as mhip_matmul_f32's addend_mode),
 // exactly the one-row decode GEMV of mhip_matmul_f32 (b f32, or bf16 bits
 // when `bf16_weights`), that also writes the RMSNorm chunk sums of squares of

@@ -49,6 +49,20 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kGemvMaxRows = 8;
+
+// The epilogue of a finished sum v with its addend element a. Modes 1 (a bias
+// row, indexed by column) and 2 (a full matrix) add it; mode 3, internal to
+// the library (the up product of a gated matmul, its addend the gate
+// product), gates the sum as the silu-mul kernel does: silu(a) * v, so the
+// gated product equals the two matmuls and silu-mul bit for bit. Modes 2 and
+// 3 index the addend as the output.
+__device__ __forceinline__ float apply_addend(float v, float a, int mode) {
+    return mode == 3 ? mhip::silu1(a) * v : v + a;
+}
+__device__ __forceinline__ float4 apply_addend(float4 v, float4 a, int mode) {
+    return make_float4(apply_addend(v.x, a.x, mode), apply_addend(v.y, a.y, mode),
+                       apply_addend(v.z, a.z, mode), apply_addend(v.w, a.w, mode));
+}
 // Largest product (m x k x n multiply-adds) that 16-32 rows run on the GEMV
 // in row blocks rather than on MFMA tiles.
 constexpr uint64_t kGemvSmallProduct = 1ull << 26;
@@ -481,7 +495,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                 if (row < M) {
                     float v = acc[i][j][r];
                     if (addend_mode == 1) v = v + addend[col];
-                    else if (addend_mode == 2) v = v + addend[row * N + col];
+                    else if (addend_mode >= 2) v = apply_addend(v, addend[row * N + col], addend_mode);
                     out[(row - out_r0) * ldo + (col - out_c0)] = v;
                 }
             }
@@ -574,9 +588,8 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* __restr
         if (addend_mode == 1) {
             const float4 b = *reinterpret_cast<const float4*>(addend + col);
             v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
-        } else if (addend_mode == 2) {
-            const float4 b = *reinterpret_cast<const float4*>(addend + i);
-            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        } else if (addend_mode >= 2) {
+            v = apply_addend(v, *reinterpret_cast<const float4*>(addend + i), addend_mode);
         }
         *reinterpret_cast<float4*>(C + i) = v;
         return;
@@ -588,7 +601,7 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* __restr
         float v = *at(w0, first, row, col);
         for (uint64_t w = w0 + 1; w <= w1; ++w) v += *at(w, first, row, col);
         if (addend_mode == 1) v = v + addend[col];
-        else if (addend_mode == 2) v = v + addend[e];
+        else if (addend_mode >= 2) v = apply_addend(v, addend[e], addend_mode);
         C[e] = v;
     }
 }
@@ -612,9 +625,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         if (addend_mode == 1) {
             const float4 b = *reinterpret_cast<const float4*>(addend + i % N);
             v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
-        } else if (addend_mode == 2) {
-            const float4 b = *reinterpret_cast<const float4*>(addend + i);
-            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+        } else if (addend_mode >= 2) {
+            v = apply_addend(v, *reinterpret_cast<const float4*>(addend + i), addend_mode);
         }
         *reinterpret_cast<float4*>(C + i) = v;
         return;
@@ -623,7 +635,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         float v = partial[e];
         for (uint32_t s = 1; s < splits; ++s) v += partial[s * total + e];
         if (addend_mode == 1) v = v + addend[e % N];
-        else if (addend_mode == 2) v = v + addend[e];
+        else if (addend_mode >= 2) v = apply_addend(v, addend[e], addend_mode);
         C[e] = v;
     }
 }
@@ -950,9 +962,8 @@ __device__ __forceinline__ void gemv_partial_body(
                 if (addend_mode == 1) {
                     const float4 b4 = *reinterpret_cast<const float4*>(addend + c);
                     v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
-                } else if (addend_mode == 2) {
-                    const float4 b4 = *reinterpret_cast<const float4*>(addend + r * N + c);
-                    v.x = v.x + b4.x; v.y = v.y + b4.y; v.z = v.z + b4.z; v.w = v.w + b4.w;
+                } else if (addend_mode >= 2) {
+                    v = apply_addend(v, *reinterpret_cast<const float4*>(addend + r * N + c), addend_mode);
                 }
                 *reinterpret_cast<float4*>(C + r * N + c) = v;
             } else {
@@ -973,7 +984,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_partial_kernel(
     A += rb * ROWS * K;
     C += rb * ROWS * N;
     if (partial) partial += rb * slices * ROWS * N;
-    if (addend_mode == 2) addend += rb * ROWS * N;
+    if (addend_mode >= 2) addend += rb * ROWS * N;
     gemv_partial_body<ROWS, BT, STREAM, CPL>(StoredRows{A, K}, NoPrologue{}, B, partial, C, K, N, k_per_slice,
                                              blockIdx.x, blockIdx.y, slices == 1, addend, addend_mode);
 }
@@ -1086,7 +1097,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     const uint64_t rb = blockIdx.z;  // row block, as in gemv_partial_kernel
     partial += rb * slices * ROWS * N;
     C += rb * ROWS * N;
-    if (addend_mode == 2) addend += rb * ROWS * N;
+    if (addend_mode >= 2) addend += rb * ROWS * N;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t col = static_cast<uint64_t>(blockIdx.x) * kGemvCols + lane * 4;
     const bool live = col < N;
@@ -1096,7 +1107,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
     for (int r = 0; r < ROWS; ++r) {
         add[r] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (wave == 0 && live && addend_mode != 0)
-            add[r] = *reinterpret_cast<const float4*>(addend + (addend_mode == 2 ? r * N : 0) + col);
+            add[r] = *reinterpret_cast<const float4*>(addend + (addend_mode >= 2 ? r * N : 0) + col);
     }
     float4 v[1][ROWS];
     gemv_reduce_sum<ROWS>({partial}, N, slices, col, live, v);
@@ -1108,7 +1119,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(
             o = make_float4(0.f, 0.f, 0.f, 0.f);
             continue;
         }
-        if (addend_mode != 0) {
+        if (addend_mode == 3) {
+            o = apply_addend(o, add[r], 3);
+        } else if (addend_mode != 0) {
             o.x = o.x + add[r].x; o.y = o.y + add[r].y; o.z = o.z + add[r].z; o.w = o.w + add[r].w;
         }
         *reinterpret_cast<float4*>(C + r * N + col) = o;
@@ -1452,7 +1465,7 @@ __global__ void fill_addend_kernel(float* C, uint64_t M, uint64_t N, const float
     if (idx >= M * N) return;
     float v = 0.0f;
     if (mode == 1) v = v + addend[idx % N];
-    else if (mode == 2) v = v + addend[idx];
+    else if (mode >= 2) v = apply_addend(v, addend[idx], mode);
     C[idx] = v;
 }
 
@@ -1529,9 +1542,9 @@ mhip_matmul_plan plan_matmul(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64
 template <class BT>
 mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, uint64_t m,
                         uint64_t k, uint64_t n, int transpose_a, int transpose_b,
-                        const float* addend, int addend_mode) {
+                        const float* addend, int addend_mode, bool gated = false) {
     MHIP_REQUIRE_CTX(ctx);
-    if (addend_mode < 0 || addend_mode > 2)
+    if (gated ? addend_mode != 3 : (addend_mode < 0 || addend_mode > 2))
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul addend mode must be 0, 1 or 2");
     if (addend_mode != 0 && !addend)
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul addend is null");
@@ -1603,6 +1616,21 @@ extern "C" mhip_status mhip_matmul_plan_f32(mhip_ctx* ctx, uint64_t m, uint64_t 
     if (!plan) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul plan: null output");
     *plan = plan_matmul(ctx, m, k, n, transpose_a != 0, transpose_b != 0, true);
     return MHIP_OK;
+}
+
+// The up product of a gated matmul (src/executor.rs:1484-1494): out =
+// silu(gate) * (a . b), gate the [m, n] gate product, through the matmul's
+// own kernels with the gate as an epilogue (addend mode 3), so it equals the
+// product followed by silu-mul bit for bit, with no [m, n] temporary for the
+// up product and no separate silu-mul launch.
+mhip_status mhip::matmul_gated_f32(mhip_ctx* ctx, const float* a, const void* b, bool bf16,
+                                   float* out, uint64_t m, uint64_t k, uint64_t n,
+                                   bool transpose_a, bool transpose_b, const float* gate) {
+    if (bf16)
+        return matmul_impl<uint16_t>(ctx, a, static_cast<const uint16_t*>(b), out, m, k, n,
+                                     transpose_a, transpose_b, gate, 3, true);
+    return matmul_impl<float>(ctx, a, static_cast<const float*>(b), out, m, k, n, transpose_a,
+                              transpose_b, gate, 3, true);
 }
 
 extern "C" mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float* out,

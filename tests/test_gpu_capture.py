@@ -124,6 +124,51 @@ def test_capture_refuses_what_it_cannot_replay(ex):
     assert ex.read_tensor("cap.new_output").shape == (2, 8)
 
 
+def test_a_captured_gated_matmul_survives_a_larger_eager_one(ex, orc):
+    """gated-matmul's matmul path keeps the gate product in a buffer the
+    executor reuses and grows. A larger eager call grows it after a step was
+    captured; the buffer the graph recorded stays valid, so replays (with
+    other inputs, eager calls in between) still equal the eager results bit
+    for bit."""
+    m, k, n = 40, 256, 344
+    x1 = orc.hashed_values(m * k, 31).reshape(m, k)
+    x2 = orc.hashed_values(m * k, 32).reshape(m, k)
+    ex.write_tensor("cg.w", orc.hashed_values(k * n, 33).reshape(k, n))
+    ex.write_tensor("cg.u", orc.hashed_values(k * n, 34).reshape(k, n))
+
+    def step():
+        ex.execute(inv("gated-matmul", ["cg.x", "cg.w", "cg.u"], "cg.out"))
+
+    def larger():
+        ex.execute(inv("gated-matmul", ["cg.bx", "cg.bw", "cg.bu"], "cg.bout"))
+        return ex.read_tensor("cg.bout")
+
+    ex.write_tensor("cg.x", x2)
+    step()
+    want2 = ex.read_tensor("cg.out")
+    ex.write_tensor("cg.x", x1)
+    step()
+    want1 = ex.read_tensor("cg.out")
+    assert not np.array_equal(bits(want1), bits(want2))
+    ex.begin_step_capture([])
+    step()
+    capture = ex.end_step_capture()
+    big_m, big_k, big_n = 400, 1024, 1900
+    ex.write_tensor("cg.bx", orc.hashed_values(big_m * big_k, 35).reshape(big_m, big_k))
+    ex.write_tensor("cg.bw", orc.hashed_values(big_k * big_n, 36).reshape(big_k, big_n))
+    ex.write_tensor("cg.bu", orc.hashed_values(big_k * big_n, 37).reshape(big_k, big_n))
+    big = larger()
+    for _ in range(3):
+        ex.replay_step(capture, 0, {"cg.x": x2})
+        assert np.array_equal(bits(ex.read_tensor("cg.out")), bits(want2))
+        assert np.array_equal(bits(larger()), bits(big))
+        ex.replay_step(capture, 0, {"cg.x": x1})
+        assert np.array_equal(bits(ex.read_tensor("cg.out")), bits(want1))
+    ex.release_step_capture(capture)
+    for name in ("cg.x", "cg.w", "cg.u", "cg.out", "cg.bx", "cg.bw", "cg.bu", "cg.bout"):
+        ex.release_tensor(name)
+
+
 def _values(count, seed):
     """The reference test's generator (src/tests_hardware_hot_path.rs:752-756)."""
     i = np.arange(count, dtype=np.int64)

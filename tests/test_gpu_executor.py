@@ -334,6 +334,58 @@ def test_gated_matmul_is_bit_identical_to_its_parts(ex, orc, rows):
         ex.release_tensor(name)
 
 
+def _bf16_exact(values):
+    return (values.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb,path", [
+    (24, 300, 512, False, False, "gemv_row_blocks"),
+    (40, 4096, 4096, False, False, "splits"),
+    (200, 2050, 1900, False, False, "stream_k"),
+    (400, 1024, 1900, False, True, "splits"),
+    (130, 512, 1901, True, True, "splits"),      # odd n: the scalar reduction
+    (4000, 64, 4064, False, True, "tiles"),
+    (301, 257, 203, True, False, None),
+])
+def test_gated_matmul_on_every_matmul_path(ex, dev, orc, m, k, n, ta, tb, path):
+    """Rows beyond the decode GEMV set run the gate product, then the up
+    product with silu(gate) applied to each finished sum: on every kernel
+    path of the matmul (row-block GEMV, whole-k splits, stream-K, direct
+    tile stores; the path is asserted) and with transposes, bit-identical to
+    matmul, matmul and silu-mul dispatched separately. Then again with a
+    compact bf16 up weight against its widened f32 form."""
+    from magnetar_hip import Boolean, ops
+    plan = ops.matmul_plan(dev, m, k, n, ta, tb)
+    if path == "gemv_row_blocks":
+        assert plan["path"] == path, plan
+    elif path is not None:
+        assert plan["path"] == "tiles", plan
+        assert (path == "stream_k") == bool(plan["stream_k"]), plan
+        assert (path == "splits") == (plan["splits"] > 1), plan
+    attrs = {"transpose_a": Boolean(ta), "transpose_b": Boolean(tb)}
+    x = orc.hashed_values(m * k, 21 + m).reshape((k, m) if ta else (m, k))
+    wg = orc.hashed_values(k * n, 22 + n).reshape((n, k) if tb else (k, n))
+    wu = _bf16_exact(orc.hashed_values(k * n, 23 + n)).reshape(wg.shape)
+    ex.write_tensor("gp.x", x)
+    ex.write_tensor("gp.g", wg)
+    ex.write_tensor("gp.u", wu)
+    ex.execute(inv("matmul", ["gp.x", "gp.g"], "gp.gate", attrs))
+    ex.execute(inv("matmul", ["gp.x", "gp.u"], "gp.up", attrs))
+    ex.execute(inv("silu-mul", ["gp.gate", "gp.up"], "gp.want"))
+    want = ex.read_tensor("gp.want")
+    ex.execute(inv("gated-matmul", ["gp.x", "gp.g", "gp.u"], "gp.out", attrs))
+    got = ex.read_tensor("gp.out")
+    print(f"[{m},{k},{n}] ta={ta} tb={tb}: {plan}")
+    assert_bitexact(got, want)
+    if ex.write_weight_tensor("gp.uc", wu):
+        ex.execute(inv("gated-matmul", ["gp.x", "gp.g", "gp.uc"], "gp.outc", attrs))
+        assert_bitexact(ex.read_tensor("gp.outc"), want)
+        ex.release_tensor("gp.uc")
+        ex.release_tensor("gp.outc")
+    for name in ("gp.x", "gp.g", "gp.u", "gp.gate", "gp.up", "gp.want", "gp.out"):
+        ex.release_tensor(name)
+
+
 def test_out_of_device_memory_is_triggered_by_a_real_over_capacity_allocation(dev, ex):
     """src/tests.rs:47-71: an allocation of 64x the device's total memory
     fails as OutOfDeviceMemory (mapped as src/error.rs:97-133); through the
