@@ -131,6 +131,55 @@ __device__ __forceinline__ void dma_tile(const float* g, uint64_t ld, uint64_t k
     }
 }
 
+// dma_tile with each lane's byte offsets within a tile (row * ld + its
+// chunk) computed once: a full tile's loads address a uniform base,
+// g + k0 * ld, plus those 32-bit offsets (the global loads' scalar-base
+// form: no per-load address arithmetic). In the last tile, rows at or past
+// `rows` repeat row rows - 1, as in dma_tile. A tile spans 32 * ld * 4
+// bytes, below 2^32 (the launch checks ld).
+template <int W>
+struct TileDma {
+    static constexpr int kChunksPerRow = W / 4;
+    static constexpr int kInstrPerWave = 32 * W / 4 / 64 / 4;
+    static_assert((kChunksPerRow & (kChunksPerRow - 1)) == 0 && kChunksPerRow >= 16,
+                  "rows of a power-of-two number of chunks, at least 16");
+    uint32_t off[kInstrPerWave];
+
+    __device__ __forceinline__ TileDma(uint64_t ld, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < kInstrPerWave; ++j) {
+            const int slot = (wave * kInstrPerWave + j) * 64 + lane;
+            const int row = slot / kChunksPerRow;
+            const int chunk = (slot % kChunksPerRow) ^ (row & 15);
+            off[j] = static_cast<uint32_t>((row * ld + chunk * 4) * sizeof(float));
+        }
+    }
+
+    __device__ __forceinline__ void load(const float* g, uint64_t ld, uint64_t k0, uint64_t rows,
+                                         float* tile, int wave, int lane) const {
+        const char* base = reinterpret_cast<const char*>(g + k0 * ld);
+        if (k0 + 32 <= rows) {
+#pragma unroll
+            for (int j = 0; j < kInstrPerWave; ++j) {
+                const int slot0 = (wave * kInstrPerWave + j) * 64;
+                __builtin_amdgcn_global_load_lds((global_void_t*)(base + off[j]),
+                                                 (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
+            }
+            return;
+        }
+        const uint32_t end = static_cast<uint32_t>(rows - 1 - k0);  // k0 < rows
+        const uint32_t row_bytes = static_cast<uint32_t>(ld * sizeof(float));
+#pragma unroll
+        for (int j = 0; j < kInstrPerWave; ++j) {
+            const int slot0 = (wave * kInstrPerWave + j) * 64;
+            const uint32_t row = static_cast<uint32_t>(slot0 + lane) / kChunksPerRow;
+            const uint32_t o = row > end ? off[j] - (row - end) * row_bytes : off[j];
+            __builtin_amdgcn_global_load_lds((global_void_t*)(base + o),
+                                             (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
+        }
+    }
+};
+
 // S^T[key][query] of one tile: A = the K rows (lane -> key l32), B = Q^T.
 template <int D>
 __device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D / 2], int l32,
@@ -254,8 +303,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
     float* const vbuf0 = lds + 2 * Cfg::kKTile;
     auto kbuf = [&](int i) { return kbuf0 + (i & 1) * Cfg::kKTile; };
     auto vbuf = [&](int i) { return vbuf0 + (i & 1) * Cfg::kVTile; };
-    auto load_k = [&](uint64_t k0, float* dst) { dma_tile<D>(K, k_ld, k0, a.kv_seq, dst, wave, lane); };
-    auto load_v = [&](uint64_t k0, float* dst) { dma_tile<VD>(V, v_ld, k0, a.kv_seq, dst, wave, lane); };
+    const TileDma<D> kdma(k_ld, wave, lane);
+    const TileDma<VD> vdma(v_ld, wave, lane);
+    auto load_k = [&](uint64_t k0, float* dst) { kdma.load(K, k_ld, k0, a.kv_seq, dst, wave, lane); };
+    auto load_v = [&](uint64_t k0, float* dst) { vdma.load(V, v_ld, k0, a.kv_seq, dst, wave, lane); };
 
     // V reads: key row `key`, column vb*32 + l32 sits in chunk
     // (vb*8 + l32/4) ^ (key & 15), and key & 15 = 8*((t/4) & 1) + 4*half +
@@ -953,7 +1004,9 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
         }
         if (st != MHIP_CAPTURE_UNSUPPORTED) return st;  // else: no decode kernel for this d
     }
-    const bool small_keys = p->kv_rows < (1ULL << 31);  // the MFMA kernel's key arithmetic is 32-bit
+    // The MFMA kernel's key arithmetic is 32-bit, and so are its byte
+    // offsets within a 32-row K or V tile.
+    const bool small_keys = p->kv_rows < (1ULL << 31) && a.kv_heads * std::max(d, vd) < (1ULL << 25);
     if (aligned && small_keys && vd == d && d == 128) return launch_prefill<128, 128>(ctx, a, batch);
     if (aligned && small_keys && vd == d && d == 64) return launch_prefill<64, 64>(ctx, a, batch);
     if (vd > 256) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention value dimension above 256");
