@@ -190,13 +190,16 @@ mhip_status mhip_matmul_f32(mhip_ctx* ctx, const float* a, const float* b, float
  * 16-byte aligned operands. No counterpart in the reference: a diagnostic for
  * tests (that a case exercises the path it is written for) and tuning.
  * path: the split-k GEMV (m <= 8), row blocks of 8 on the GEMV (16-32 rows of
- * a small product), or MFMA tiles of tile_m x tile_n with `waves` waves per
+ * a small product with k > 1024), one launch of 32 x 32 MFMA tiles with k
+ * split over the workgroup's waves (16-32 rows of a small product, k <= 1024,
+ * k % 4 == 0), or MFMA tiles of tile_m x tile_n with `waves` waves per
  * workgroup. splits: k slices of the GEMV, or k splits of the tiles (1: none);
  * stream_k: 1 when (tile, k slice) runs are dealt to the workgroups. */
 enum {
     MHIP_MATMUL_PATH_GEMV = 0,
     MHIP_MATMUL_PATH_GEMV_ROW_BLOCKS = 1,
-    MHIP_MATMUL_PATH_TILES = 2
+    MHIP_MATMUL_PATH_TILES = 2,
+    MHIP_MATMUL_PATH_SMALL_TILES = 3
 };
 typedef struct {
     uint32_t path;

@@ -1458,6 +1458,181 @@ mhip_status dispatch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, 
     }
 }
 
+// Small products of 16-32 rows in one launch (no partial sums, no reduction
+// launch): a workgroup of kSmallWaves waves owns a 32 x 32 tile of C. Wave w
+// takes k range [w * kq, (w + 1) * kq) (kq a multiple of 8; the last ranges
+// short or empty) and sums it with v_mfma_f32_32x32x2_f32 in the k order
+// 8g + 4h + e of the MFMA tiles: lane half h feeds A[row][g + 4h + e] from one
+// 16-byte load and B[g + 4h + e][col]. Loads go out two k groups at a time.
+// The waves' partial tiles meet in LDS and wave r adds register row r over
+// the waves in wave order. Each output's sum depends only on its own row and
+// column, so any row subset of a product taking this path gives the same
+// bits, and a set of products (the GEMV sets' epilogues) the bits of each.
+constexpr int kSmallWaves = 16;
+constexpr uint64_t kSmallMaxK = 1024;
+static_assert(kSmallWaves == 16, "one register row of the 32 x 32 tile per wave");
+
+// The tile's sums at (small_row(row0), col0 + lane % 32) for the calling
+// wave; every thread of the workgroup calls it (it synchronises).
+template <class BT>
+__device__ __forceinline__ float small_tile(const float* __restrict__ A, const BT* __restrict__ B,
+                                            uint64_t M, uint64_t K, uint64_t N, uint64_t kq,
+                                            uint64_t row0, uint64_t col0,
+                                            float (*red)[16][64]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const uint64_t kb = wave * kq, ke = min(K, kb + kq);
+    const uint64_t arow = row0 + l32, bcol = col0 + l32;
+    const bool arow_ok = arow < M, bcol_ok = bcol < N;
+    const float* ap = A + arow * K;
+    v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    constexpr int kBatch = 2;  // k groups of 8 per batch of loads
+    for (uint64_t g0 = kb; g0 < ke; g0 += 8 * kBatch) {
+        float4 a4[kBatch];
+        float bv[kBatch][4];
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+            const uint64_t kk = g0 + 8 * t + 4 * h;  // K % 4 == 0: all four or none
+            a4[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (arow_ok && kk < ke) a4[t] = *reinterpret_cast<const float4*>(ap + kk);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                bv[t][e] = (bcol_ok && kk + e < ke) ? elem(B + (kk + e) * N + bcol) : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].x, bv[t][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].y, bv[t][1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].z, bv[t][2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].w, bv[t][3], acc, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    float v = red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < kSmallWaves; ++w) v += red[w][wave][lane];
+    __syncthreads();  // the caller may sum another tile through `red`
+    return v;
+}
+
+// Register row r = wave of the tile holds row row0 + 8 (r / 4) + 4h + r % 4.
+__device__ __forceinline__ uint64_t small_row(uint64_t row0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return row0 + 8 * (wave / 4) + 4 * (lane >> 5) + (wave % 4);
+}
+
+template <class BT>
+__global__ __launch_bounds__(64 * kSmallWaves) void small_mfma_kernel(
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, uint64_t M,
+    uint64_t K, uint64_t N, uint64_t kq, const float* __restrict__ addend, int addend_mode) {
+    __shared__ float red[kSmallWaves][16][64];
+    const uint64_t col0 = static_cast<uint64_t>(blockIdx.x) * 32;
+    const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * 32;
+    float v = small_tile<BT>(A, B, M, K, N, kq, row0, col0, red);
+    const uint64_t row = small_row(row0), col = col0 + (threadIdx.x & 31);
+    if (row >= M || col >= N) return;
+    if (addend_mode == 1) v = v + addend[col];
+    else if (addend_mode >= 2) v = apply_addend(v, addend[row * N + col], addend_mode);
+    C[row * N + col] = v;
+}
+
+// A GEMV set (gemv_set_f32) of 16-32 rows on the small tiles: workgroup x
+// takes a 32-column tile of one target (targets' tiles in order); with the
+// silu-mul epilogue the workgroup sums the gate tile, then the up tile of the
+// same columns, and stores silu(gate) * up; with the RoPE epilogue targets 0
+// and 1 rotate each interleaved pair (columns 2i, 2i + 1, in lanes l, l ^ 1)
+// with the factors of the vector RoPE kernel. Each target's sums are those of
+// small_mfma_kernel for it alone.
+struct SmallSeg {
+    const void* b;
+    float* out;
+    const uint64_t* out_advance;  // captured step: rows of `out` move by the replay offset
+    uint64_t n;
+    uint32_t first_tile;
+};
+
+struct SmallSet {
+    SmallSeg seg[3];
+    int count;
+};
+
+__device__ __forceinline__ SmallSeg pick(const SmallSet& set, int i) {
+    if (i == 0) return set.seg[0];
+    if (i == 1) return set.seg[1];
+    return set.seg[2];
+}
+
+template <class BT>
+__global__ __launch_bounds__(64 * kSmallWaves) void small_mfma_set_kernel(
+    const float* __restrict__ A, uint64_t M, uint64_t K, uint64_t kq, SmallSet set, int epilogue,
+    RopeEpi rope_q, RopeEpi rope_k) {
+    __shared__ float red[kSmallWaves][16][64];
+    const uint32_t b = blockIdx.x;
+    const int i = (set.count > 2 && b >= set.seg[2].first_tile) ? 2
+                  : (set.count > 1 && b >= set.seg[1].first_tile) ? 1 : 0;
+    const SmallSeg s = pick(set, i);
+    const int l32 = threadIdx.x & 31;
+    const uint64_t col0 = static_cast<uint64_t>(b - s.first_tile) * 32;
+    const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * 32;
+    const uint64_t row = small_row(row0), col = col0 + l32;
+    float v = small_tile<BT>(A, static_cast<const BT*>(s.b), M, K, s.n, kq, row0, col0, red);
+    if (epilogue == mhip::kGemvSiluMul) {
+        const SmallSeg u = pick(set, 1);
+        const float up = small_tile<BT>(A, static_cast<const BT*>(u.b), M, K, u.n, kq, row0, col0, red);
+        v = mhip::silu1(v) * up;
+    } else if (epilogue == mhip::kGemvRopeQK && i < 2) {
+        const float other = __shfl_xor(v, 1, 64);  // the pair's other column
+        const RopeEpi& e = i == 0 ? rope_q : rope_k;
+        const uint64_t j = col % e.head_width;
+        if (j < e.dimension) {
+            const uint64_t p = j / 2;
+            const float position =
+                mhip::rope_position(e.offset + (e.advance ? *e.advance : 0), row, e.scale);
+            float c, sn;
+            mhip::rope_freq_cs(position, e.table[p], e.table[e.half + p], &c, &sn);
+            const bool even = (l32 & 1) == 0;
+            float re, ro;
+            mhip::rope_rotate(even ? v : other, even ? other : v, c, sn, &re, &ro);
+            v = even ? re : ro;
+        }
+    }
+    if (row >= M || col >= s.n) return;
+    float* out = s.out + (s.out_advance ? *s.out_advance : 0) * s.n;
+    out[row * s.n + col] = v;
+}
+
+// Whether a product of a few rows takes small_mfma_kernel: A's 16-byte loads
+// need k % 4 == 0 and an aligned base; past kSmallMaxK the waves' 4-byte B
+// loads make it slower than the row-blocked GEMV.
+bool small_mfma_fits(uint64_t k, bool a_aligned) {
+    return k % 4 == 0 && k <= kSmallMaxK && a_aligned;
+}
+
+template <class BT>
+mhip_status launch_small_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, uint64_t m,
+                              uint64_t k, uint64_t n, const float* addend, int mode) {
+    const uint64_t kq = (k + 8 * kSmallWaves - 1) / (8 * kSmallWaves) * 8;
+    const dim3 grid(static_cast<unsigned>((n + 31) / 32), static_cast<unsigned>((m + 31) / 32));
+    hipLaunchKernelGGL(small_mfma_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, ctx->stream, a, b, c,
+                       m, k, n, kq, addend, mode);
+    return mhip::check_launch("matmul (small MFMA tiles)");
+}
+
+template <class BT>
+mhip_status launch_small_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t k,
+                             const SmallSet& set, uint64_t tiles, int epilogue, const RopeEpi& rq,
+                             const RopeEpi& rk) {
+    const uint64_t kq = (k + 8 * kSmallWaves - 1) / (8 * kSmallWaves) * 8;
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>((rows + 31) / 32));
+    hipLaunchKernelGGL(small_mfma_set_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, ctx->stream, a,
+                       rows, k, kq, set, epilogue, rq, rk);
+    return mhip::check_launch("GEMV set (small MFMA tiles)");
+}
+
 // Zero-inner-dimension product: C = 0 (+ addend).
 __global__ void fill_addend_kernel(float* C, uint64_t M, uint64_t N, const float* addend,
                                    int mode) {
@@ -1517,6 +1692,13 @@ mhip_matmul_plan plan_matmul(const mhip_ctx* ctx, uint64_t m, uint64_t k, uint64
     }
     if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= kGemvSmallProduct && !ta &&
         !tb && n % 4 == 0 && b_aligned) {
+        if (small_mfma_fits(k, true)) {
+            out.path = MHIP_MATMUL_PATH_SMALL_TILES;
+            out.tile_m = out.tile_n = 32;
+            out.waves = kSmallWaves;
+            out.splits = 1;
+            return out;
+        }
         uint64_t slices, per;
         gemv_slicing(ctx, k, n, &slices, &per);
         out.path = MHIP_MATMUL_PATH_GEMV_ROW_BLOCKS;
@@ -1563,11 +1745,15 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
     if (m <= kGemvMaxRows && !ta && !tb && n % 4 == 0 && b_aligned)
         return dispatch_gemv<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
     // A few rows of a small product (up to 32 rows in blocks of 8, at most
-    // 2^26 multiply-adds): the GEMV's two short launches beat MFMA tiles that
-    // would be three quarters padding and walk k serially.
+    // 2^26 multiply-adds): one launch of small_mfma_kernel up to k = 1024,
+    // else the GEMV's two short launches; both beat MFMA tiles that would be
+    // three quarters padding and walk k serially.
     if (m <= 4 * kGemvMaxRows && m % kGemvMaxRows == 0 && m * k * n <= kGemvSmallProduct && !ta && !tb &&
-        n % 4 == 0 && b_aligned)
+        n % 4 == 0 && b_aligned) {
+        if (small_mfma_fits(k, mhip::aligned16(a)))
+            return launch_small_mfma<BT>(ctx, a, b, out, m, k, n, addend, addend_mode);
         return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
+    }
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
     const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
     switch (choose_tiles(ctx, m, k, n)) {
@@ -1948,6 +2134,28 @@ mhip_status gemv_set_f32(mhip_ctx* ctx, const float* a, uint64_t rows, uint64_t 
             e.scale = q.scale;
             e.advance = advance_ptr(ctx, MHIP_ADVANCE_POSITION_OFFSET, UINT64_MAX);
         }
+    }
+    // 16-32 rows whose products take small_mfma_kernel as separate matmuls
+    // take its set form (the same sums), in one launch.
+    if (rows > kGemvMaxRows && norm_mode == 0 && small_mfma_fits(k, aligned16(a))) {
+        SmallSet ss{};
+        ss.count = count;
+        uint64_t tiles = 0;
+        for (int i = 0; i < count; ++i) {
+            SmallSeg& g = ss.seg[i];
+            g.b = targets[i].b;
+            g.out = targets[i].out;
+            g.out_advance = set.seg[i].out_advance;
+            g.n = targets[i].n;
+            if (epilogue == kGemvSiluMul && i == 1) {
+                g.first_tile = UINT32_MAX;  // summed with the gate's tiles
+                continue;
+            }
+            g.first_tile = static_cast<uint32_t>(tiles);
+            tiles += (targets[i].n + 31) / 32;
+        }
+        return bf16_weights ? launch_small_set<uint16_t>(ctx, a, rows, k, ss, tiles, epilogue, rq, rk)
+                            : launch_small_set<float>(ctx, a, rows, k, ss, tiles, epilogue, rq, rk);
     }
     void* scratch = nullptr;
     mhip_status st = workspace(ctx, floats * sizeof(float), &scratch);

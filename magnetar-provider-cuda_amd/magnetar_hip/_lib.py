@@ -80,7 +80,7 @@ class MatmulPlan(ctypes.Structure):
                 ("waves", ctypes.c_uint32), ("splits", ctypes.c_uint32), ("stream_k", ctypes.c_uint32)]
 
 
-MATMUL_PATHS = {0: "gemv", 1: "gemv_row_blocks", 2: "tiles"}
+MATMUL_PATHS = {0: "gemv", 1: "gemv_row_blocks", 2: "tiles", 3: "small_tiles"}
 
 
 class AttentionParams(ctypes.Structure):

@@ -198,8 +198,9 @@ def test_fused_block_is_bit_identical_to_the_separate_calls(dev, orc, seq, posit
     gate/up launch; Q/K/V GEMVs with RoPE in the reduction, gate/up GEMVs with
     silu * up) change launches, not arithmetic: the block output and the
     cache rows equal the unfused chain's bit for bit. 16-32 rows take the sets
-    in row blocks of 8; 20 and 40 rows take the separate calls in the block
-    too. Hidden 256/512 normalise a row with one wave, 2048/4096 with a
+    on one-launch MFMA tiles where k <= 1024 (Q/K/V, O, gate/up here) and in
+    row blocks of 8 on the GEMV otherwise (the down projection's k = 1376);
+    20 and 40 rows take the separate calls in the block too. Hidden 256/512 normalise a row with one wave, 2048/4096 with a
     workgroup of four."""
     from magnetar_hip.decoder import DecoderBlock, Shapes
     head_dim = 64 if hidden <= 512 else 128

@@ -339,7 +339,8 @@ def _bf16_exact(values):
 
 
 @pytest.mark.parametrize("m,k,n,ta,tb,path", [
-    (24, 300, 512, False, False, "gemv_row_blocks"),
+    (24, 300, 512, False, False, "small_tiles"),
+    (16, 1100, 512, False, False, "gemv_row_blocks"),
     (40, 4096, 4096, False, False, "splits"),
     (200, 2050, 1900, False, False, "stream_k"),
     (400, 1024, 1900, False, True, "splits"),
@@ -348,15 +349,17 @@ def _bf16_exact(values):
     (301, 257, 203, True, False, None),
 ])
 def test_gated_matmul_on_every_matmul_path(ex, dev, orc, m, k, n, ta, tb, path):
-    """Rows beyond the decode GEMV set run the gate product, then the up
-    product with silu(gate) applied to each finished sum: on every kernel
-    path of the matmul (row-block GEMV, whole-k splits, stream-K, direct
-    tile stores; the path is asserted) and with transposes, bit-identical to
-    matmul, matmul and silu-mul dispatched separately. Then again with a
-    compact bf16 up weight against its widened f32 form."""
+    """Up to 32 rows of small products take the GEMV set (on one-launch
+    small MFMA tiles or row blocks of 8, as the matmul would); other shapes
+    run the gate product, then the up product with silu(gate) applied to
+    each finished sum: on every kernel path of the matmul (whole-k splits,
+    stream-K, direct tile stores; the path is asserted) and with transposes.
+    Each is bit-identical to matmul, matmul and silu-mul dispatched
+    separately; then again with a compact bf16 up weight against its
+    widened f32 form."""
     from magnetar_hip import Boolean, ops
     plan = ops.matmul_plan(dev, m, k, n, ta, tb)
-    if path == "gemv_row_blocks":
+    if path in ("gemv_row_blocks", "small_tiles"):
         assert plan["path"] == path, plan
     elif path is not None:
         assert plan["path"] == "tiles", plan

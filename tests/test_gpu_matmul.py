@@ -181,12 +181,13 @@ def test_large_tile_path_ragged_edges_and_addends(dev, orc, m, k, n, mode):
         assert np.array_equal(got.view(np.uint32), summed.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,k,n,mode", [(16, 256, 256, 0), (24, 688, 256, 1), (32, 256, 688, 2),
-                                        (32, 100, 300, 0), (16, 4096, 1024, 2)])
+@pytest.mark.parametrize("m,k,n,mode", [(16, 1028, 256, 0), (24, 1100, 256, 1), (32, 258, 688, 2),
+                                        (32, 102, 300, 0), (16, 4096, 1024, 2)])
 def test_row_blocked_gemv(dev, orc, m, k, n, mode):
-    """Small products of 16-32 rows run as blocks of 8 rows on the split-k
-    GEMV: against the oracle, and each block of 8 rows bit-identical to the
-    8-row GEMV of those rows alone (same slicing of k, same summation order)."""
+    """Small products of 16-32 rows with k > 1024 or k % 4 != 0 run as blocks
+    of 8 rows on the split-k GEMV: against the oracle, and each block of 8
+    rows bit-identical to the 8-row GEMV of those rows alone (same slicing of
+    k, same summation order)."""
     from magnetar_hip import ops
     assert ops.matmul_plan(dev, m, k, n)["path"] == "gemv_row_blocks"
     assert ops.matmul_plan(dev, 8, k, n)["path"] == "gemv"
@@ -212,6 +213,45 @@ def test_row_blocked_gemv(dev, orc, m, k, n, mode):
         block = ops.matmul(dev, dev.upload(np.ascontiguousarray(a[r:r + 8])), db, addend=part,
                            addend_mode=mode).numpy()
         assert_bitexact(got[r:r + 8], block)
+
+
+@pytest.mark.parametrize("m,k,n,mode", [(16, 256, 256, 0), (24, 688, 256, 1), (32, 256, 688, 2),
+                                        (32, 100, 300, 0), (32, 1024, 2048, 2), (16, 4, 36, 1),
+                                        (24, 1024, 4, 0)])
+def test_small_mfma_tiles(dev, orc, m, k, n, mode):
+    """Small products of 16-32 rows with k <= 1024 (k % 4 == 0) run in one
+    launch of 32 x 32 MFMA tiles, k split over the workgroup's 16 waves:
+    against the oracle (both addend forms), ragged column tiles and short
+    last k ranges included, and every 16-row block bit-identical to the
+    product of those rows alone (an output's sum depends only on its own row
+    and column)."""
+    from magnetar_hip import ops
+    plan = ops.matmul_plan(dev, m, k, n)
+    assert plan["path"] == "small_tiles" and plan["tile"] == (32, 32) and plan["waves"] == 16, plan
+    a = orc.uniform(m * k, 45 + m, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 46 + n, -1.0, 1.0).reshape(k, n)
+    addend = None
+    if mode == 1:
+        addend = orc.uniform(n, 47, -1.0, 1.0)
+    elif mode == 2:
+        addend = orc.uniform(m * n, 48, -1.0, 1.0).reshape(m, n)
+    db = dev.upload(b)
+    got = ops.matmul(dev, dev.upload(a), db, addend=dev.upload(addend) if addend is not None else None,
+                     addend_mode=mode).numpy()
+    want, st = orc.matmul(a, b, addend=addend, addend_mode=mode)
+    assert st == 0
+    err = max_normwise_err(got, want)
+    print(f"small tiles [{m},{k},{n}] mode {mode}: normwise err {err:.2e}")
+    assert err <= TOL
+    for r in range(0, m - 15, 8):
+        part = None
+        if mode == 1:
+            part = dev.upload(addend)
+        elif mode == 2:
+            part = dev.upload(np.ascontiguousarray(addend[r:r + 16]))
+        block = ops.matmul(dev, dev.upload(np.ascontiguousarray(a[r:r + 16])), db, addend=part,
+                           addend_mode=mode).numpy()
+        assert_bitexact(got[r:r + 16], block)
 
 
 @pytest.mark.parametrize("m,k,n,mode,tile,stream", [
