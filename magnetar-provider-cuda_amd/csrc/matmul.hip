@@ -1473,50 +1473,72 @@ constexpr uint64_t kSmallMaxK = 1024;
 static_assert(kSmallWaves == 16, "one register row of the 32 x 32 tile per wave");
 
 // The tile's sums at (small_row(row0), col0 + lane % 32) for the calling
-// wave; every thread of the workgroup calls it (it synchronises).
-template <class BT>
-__device__ __forceinline__ float small_tile(const float* __restrict__ A, const BT* __restrict__ B,
-                                            uint64_t M, uint64_t K, uint64_t N, uint64_t kq,
-                                            uint64_t row0, uint64_t col0,
-                                            float (*red)[16][64]) {
+// wave, of A times each of the T matrices B[t] (same shape; T = 2 for a
+// gate/up pair shares A's loads and issues both matrices' loads together).
+// Every thread of the workgroup calls it (it synchronises).
+template <class BT, int T>
+__device__ __forceinline__ void small_tiles(const float* __restrict__ A,
+                                            const BT* const (&B)[T], uint64_t M, uint64_t K,
+                                            uint64_t N, uint64_t kq, uint64_t row0, uint64_t col0,
+                                            float (*red)[16][64], float (&out)[T]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const uint64_t kb = wave * kq, ke = min(K, kb + kq);
     const uint64_t arow = row0 + l32, bcol = col0 + l32;
     const bool arow_ok = arow < M, bcol_ok = bcol < N;
     const float* ap = A + arow * K;
-    v16f acc;
+    v16f acc[T];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int m = 0; m < T; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
     constexpr int kBatch = 2;  // k groups of 8 per batch of loads
     for (uint64_t g0 = kb; g0 < ke; g0 += 8 * kBatch) {
         float4 a4[kBatch];
-        float bv[kBatch][4];
+        float bv[T][kBatch][4];
 #pragma unroll
         for (int t = 0; t < kBatch; ++t) {
             const uint64_t kk = g0 + 8 * t + 4 * h;  // K % 4 == 0: all four or none
             a4[t] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (arow_ok && kk < ke) a4[t] = *reinterpret_cast<const float4*>(ap + kk);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                bv[t][e] = (bcol_ok && kk + e < ke) ? elem(B + (kk + e) * N + bcol) : 0.0f;
+            for (int m = 0; m < T; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    bv[m][t][e] = (bcol_ok && kk + e < ke) ? elem(B[m] + (kk + e) * N + bcol) : 0.0f;
         }
 #pragma unroll
-        for (int t = 0; t < kBatch; ++t) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].x, bv[t][0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].y, bv[t][1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].z, bv[t][2], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].w, bv[t][3], acc, 0, 0, 0);
-        }
+        for (int m = 0; m < T; ++m)
+#pragma unroll
+            for (int t = 0; t < kBatch; ++t) {
+                acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].x, bv[m][t][0], acc[m], 0, 0, 0);
+                acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].y, bv[m][t][1], acc[m], 0, 0, 0);
+                acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].z, bv[m][t][2], acc[m], 0, 0, 0);
+                acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[t].w, bv[m][t][3], acc[m], 0, 0, 0);
+            }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
-    __syncthreads();
-    float v = red[0][wave][lane];
+    for (int m = 0; m < T; ++m) {
 #pragma unroll
-    for (int w = 1; w < kSmallWaves; ++w) v += red[w][wave][lane];
-    __syncthreads();  // the caller may sum another tile through `red`
-    return v;
+        for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[m][r];
+        __syncthreads();
+        float v = red[0][wave][lane];
+#pragma unroll
+        for (int w = 1; w < kSmallWaves; ++w) v += red[w][wave][lane];
+        out[m] = v;
+        __syncthreads();  // `red` is written again
+    }
+}
+
+template <class BT>
+__device__ __forceinline__ float small_tile(const float* __restrict__ A, const BT* __restrict__ B,
+                                            uint64_t M, uint64_t K, uint64_t N, uint64_t kq,
+                                            uint64_t row0, uint64_t col0,
+                                            float (*red)[16][64]) {
+    const BT* const bs[1] = {B};
+    float v[1];
+    small_tiles<BT, 1>(A, bs, M, K, N, kq, row0, col0, red, v);
+    return v[0];
 }
 
 // Register row r = wave of the tile holds row row0 + 8 (r / 4) + 4h + r % 4.
@@ -1542,8 +1564,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_mfma_kernel(
 
 // A GEMV set (gemv_set_f32) of 16-32 rows on the small tiles: workgroup x
 // takes a 32-column tile of one target (targets' tiles in order); with the
-// silu-mul epilogue the workgroup sums the gate tile, then the up tile of the
-// same columns, and stores silu(gate) * up; with the RoPE epilogue targets 0
+// silu-mul epilogue the workgroup sums the gate and up tiles of the same
+// columns together and stores silu(gate) * up; with the RoPE epilogue targets 0
 // and 1 rotate each interleaved pair (columns 2i, 2i + 1, in lanes l, l ^ 1)
 // with the factors of the vector RoPE kernel. Each target's sums are those of
 // small_mfma_kernel for it alone.
@@ -1579,12 +1601,17 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_mfma_set_kernel(
     const uint64_t col0 = static_cast<uint64_t>(b - s.first_tile) * 32;
     const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * 32;
     const uint64_t row = small_row(row0), col = col0 + l32;
-    float v = small_tile<BT>(A, static_cast<const BT*>(s.b), M, K, s.n, kq, row0, col0, red);
+    float v;
     if (epilogue == mhip::kGemvSiluMul) {
-        const SmallSeg u = pick(set, 1);
-        const float up = small_tile<BT>(A, static_cast<const BT*>(u.b), M, K, u.n, kq, row0, col0, red);
-        v = mhip::silu1(v) * up;
-    } else if (epilogue == mhip::kGemvRopeQK && i < 2) {
+        // Gate (segment 0) and up (segment 1, the same columns) summed together.
+        const BT* const bs[2] = {static_cast<const BT*>(s.b), static_cast<const BT*>(set.seg[1].b)};
+        float gu[2];
+        small_tiles<BT, 2>(A, bs, M, K, s.n, kq, row0, col0, red, gu);
+        v = mhip::silu1(gu[0]) * gu[1];
+    } else {
+        v = small_tile<BT>(A, static_cast<const BT*>(s.b), M, K, s.n, kq, row0, col0, red);
+    }
+    if (epilogue == mhip::kGemvRopeQK && i < 2) {
         const float other = __shfl_xor(v, 1, 64);  // the pair's other column
         const RopeEpi& e = i == 0 ? rope_q : rope_k;
         const uint64_t j = col % e.head_width;

@@ -427,3 +427,59 @@ def test_a_captured_decoder_block_replays_decode_steps(dev, orc, hidden, heads, 
         graph.launch(rows - P)  # past the cache
     dev.check_flags()
     graph.close()
+
+
+def test_a_captured_decoder_block_replays_a_prefill_chunk(dev, orc):
+    """A 16-token chunk of the block (its Q/K/V and gate/up sets and the O and
+    down products on the one-launch small MFMA tiles, RoPE and the K/V cache
+    append in the set's epilogue) captured at position P replays with new
+    tokens: each replay equals the eager block at P bit for bit, and the
+    oracle's block within 1e-4. Several query rows replay only at offset 0
+    (src/kernels.rs:6661-6667), so the graph refuses any other."""
+    import magnetar_hip
+    from magnetar_hip import ops
+    from magnetar_hip.decoder import DecoderBlock, Shapes
+    from magnetar_hip.device import (ADVANCE_KEY_COUNT, ADVANCE_POSITION_OFFSET,
+                                     ADVANCE_ROW_OFFSET)
+    from reference_chain import reference_block
+    s = Shapes(vocab=512, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512)
+    assert ops.matmul_plan(dev, 16, 256, 512)["path"] == "small_tiles"
+    seq, rows, P = 16, 64, 8
+    w = {}
+    for i, (name, shape) in enumerate(s.weight_shapes().items()):
+        n = int(np.prod(shape))
+        w[name] = (orc.normal(n, 900 + i, 1.0, 0.1) if name.endswith("norm")
+                   else orc.normal(n, 900 + i, 0.0, 0.05)).reshape(shape)
+    kw = s.kv_heads * s.head_dim
+    history_k = orc.normal(rows * kw, 990, 0.0, 0.5).reshape(rows, kw)
+    history_v = orc.normal(rows * kw, 991, 0.0, 0.5).reshape(rows, kw)
+    ids = [orc.token_ids(seq, 1000 + i, 512) for i in range(3)]
+
+    eager_block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=seq)
+    eager = []
+    for i in range(3):
+        eager_block.k_cache, eager_block.v_cache = dev.upload(history_k), dev.upload(history_v)
+        out = eager_block.forward(dev.upload(ids[i]), P).numpy()
+        eager.append((out, eager_block.k_cache.numpy(), eager_block.v_cache.numpy()))
+        want, _, _ = reference_block(orc, s, w, ids[i], P, history_k.copy(), history_v.copy())
+        assert max_normwise_err(out, want) <= 1e-4
+
+    block = DecoderBlock(dev, s, w, cache_rows=rows, max_seq=seq)
+    block.k_cache, block.v_cache = dev.upload(history_k), dev.upload(history_v)
+    ids_buf = dev.upload(ids[0])
+    out = dev.empty((seq, s.hidden))
+    block.forward(ids_buf, P, out)  # sizes scratch and caches the RoPE table
+    dev.capture_begin(ADVANCE_POSITION_OFFSET | ADVANCE_KEY_COUNT | ADVANCE_ROW_OFFSET)
+    block.forward(ids_buf, P, out)
+    graph = dev.capture_end()
+    assert graph.max_offset == 0
+    for i in (1, 0, 2, 1):
+        dev.write(ids_buf, ids[i])
+        graph.launch(0)
+        assert np.array_equal(bits(out.numpy()), bits(eager[i][0])), i
+        assert np.array_equal(bits(block.k_cache.numpy()), bits(eager[i][1])), i
+        assert np.array_equal(bits(block.v_cache.numpy()), bits(eager[i][2])), i
+    with pytest.raises(magnetar_hip.MagnetarHipError):
+        graph.launch(1)
+    dev.check_flags()
+    graph.close()
