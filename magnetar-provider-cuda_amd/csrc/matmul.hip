@@ -29,12 +29,15 @@
 //    equal runs of (tile, k slice) units per workgroup (stream-K) when the
 //    tiles divide the device badly; partial tiles go to a workspace and a
 //    second launch adds them in k order (deterministic) with the addend.
-//  - m <= kGemvMaxRows (decode), or up to 32 rows of a small product in row
-//    blocks of 8: the work is reading B once (HBM-bound), so each wave
-//    streams 256 columns of B (512 for compact bf16 weights on up to 4 rows)
-//    with 16-byte loads over one k slice, keeping m x 4 partial sums per
-//    lane; partial sums per k slice go to a workspace and a second launch
-//    adds them in a fixed order (deterministic), four waves per 256 columns.
+//  - m <= kGemvMaxRows (decode), or up to 32 rows of a small product with
+//    k > 1024 in row blocks of 8: the work is reading B once (HBM-bound), so
+//    each wave streams 256 columns of B (512 for compact bf16 weights on up
+//    to 4 rows) with 16-byte loads over one k slice, keeping m x 4 partial
+//    sums per lane; partial sums per k slice go to a workspace and a second
+//    launch adds them in a fixed order (deterministic), four waves per 256
+//    columns.
+//  - 16-32 rows of a small product with k <= 1024: one launch of 32 x 32
+//    MFMA tiles whose 16 waves split k and meet in LDS (small_mfma_kernel).
 #include <type_traits>
 
 #include "common.hpp"
@@ -63,8 +66,8 @@ __device__ __forceinline__ float4 apply_addend(float4 v, float4 a, int mode) {
     return make_float4(apply_addend(v.x, a.x, mode), apply_addend(v.y, a.y, mode),
                        apply_addend(v.z, a.z, mode), apply_addend(v.w, a.w, mode));
 }
-// Largest product (m x k x n multiply-adds) that 16-32 rows run on the GEMV
-// in row blocks rather than on MFMA tiles.
+// Largest product (m x k x n multiply-adds) that 16-32 rows run on the small
+// MFMA tiles or the GEMV's row blocks rather than on the large MFMA tiles.
 constexpr uint64_t kGemvSmallProduct = 1ull << 26;
 
 // Split-k partial sums live in the context's workspace; stream order makes
