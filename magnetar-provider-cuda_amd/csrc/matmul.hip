@@ -1882,9 +1882,13 @@ mhip_status mhip::noalloc_scratch(mhip_ctx* ctx, float** out) {
     std::lock_guard<std::mutex> lock(scratch_mutex);
     float*& address = scratch_address[ctx->device];
     if (!address) {
-        hipError_t err = hipSetDevice(ctx->device);
+        // The caller's current device is put back afterwards.
+        int previous = -1;
+        hipError_t err = hipGetDevice(&previous);
+        if (err == hipSuccess) err = hipSetDevice(ctx->device);
         void* p = nullptr;
         if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (previous >= 0 && previous != ctx->device) (void)hipSetDevice(previous);
         if (err != hipSuccess) return mhip::from_hip(err, "locating the allocation-free matmul's scratch");
         address = static_cast<float*>(p);
     }
