@@ -72,14 +72,19 @@ class Case:
         # such as the C1 block) is timed over 5 such windows and the median
         # window counts, to damp the noise of one short window. Every window
         # times exactly `steps` launches between synchronisations.
-        times = []
+        # The host's own time to enqueue a launch (the calls return before
+        # the GPU finishes) is kept beside it: what a host loop pays per call.
+        times, host = [], []
         while not times or (times[0] * steps < 5.0 and len(times) < 5):
             dev.timer_start()
+            t0 = time.perf_counter()
             for j in range(steps):
                 self.launch(warmup + len(times) * steps + j)
+            host.append((time.perf_counter() - t0) / steps)
             times.append(dev.timer_stop() / steps)
         windows = len(times)
         ms = sorted(times)[windows // 2]
+        host_us = sorted(host)[windows // 2] * 1e6
         if self.bound == "hbm":
             achieved = self.work / (ms * 1e-3) / 1e9
             peak, unit = HBM_PEAK_GBS, "GB/s"
@@ -88,7 +93,7 @@ class Case:
             peak, unit = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
         out = {"ms": ms, "achieved": achieved, "unit": unit, "peak": peak,
                "frac": achieved / peak, "work": self.work, "bound": self.bound,
-               "shape": self.shape, "windows": windows}
+               "shape": self.shape, "windows": windows, "host_us": round(host_us, 2)}
         if self.tokens:
             out["tokens_per_s"] = self.tokens / (ms * 1e-3)
         return out
@@ -632,7 +637,8 @@ def main(argv=None):
         r = results[case.name]
         extra = f"  {r['tokens_per_s']:10.1f} tokens/s" if "tokens_per_s" in r else ""
         print(f"# {case.name:14s} {r['ms']*1e3:9.1f} us  {r['achieved']:8.1f} {r['unit']}  "
-              f"{100*r['frac']:5.1f}% of {r['bound']}{extra}", file=sys.stderr, flush=True)
+              f"{100*r['frac']:5.1f}% of {r['bound']}{extra}  host {r['host_us']:.1f} us/call",
+              file=sys.stderr, flush=True)
     dev.check_flags()
 
     head = results.get(HEADLINE)
@@ -674,7 +680,7 @@ def main(argv=None):
                    "compute_units": info["compute_units"]},
         "kernels": {k: dict({"ms": round(v["ms"], 5), "achieved": round(v["achieved"], 2),
                              "unit": v["unit"], "frac": round(v["frac"], 4), "shape": v["shape"],
-                             "windows": v["windows"]},
+                             "windows": v["windows"], "host_us": v["host_us"]},
                             **({"tokens_per_s": round(v["tokens_per_s"], 1)}
                                if "tokens_per_s" in v else {}),
                             **({"cpu": v["cpu"]} if "cpu" in v else {}))
