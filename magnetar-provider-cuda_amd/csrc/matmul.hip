@@ -10,7 +10,7 @@
 //    orientation, unpadded: rows along k (B stored [k, n], A stored [k, m])
 //    as they are, rows along m or n (A stored [m, k], B stored [n, k]) with
 //    their 16-byte chunks XOR-swizzled. Interior slices of f32 operands go
-//    straight from global memory to LDS (global_load_lds_dwordx4: no
+//    straight from global memory to LDS (buffer_load_dwordx4 with the lds bit: no
 //    registers, no LDS write instructions) while the MFMAs run on the other
 //    buffer; edge and partial slices, and compact bf16 B, go through
 //    registers (zero-filled, widened) and one 16-byte LDS write per chunk.
@@ -39,6 +39,8 @@
 //  - 16-32 rows of a small product with k <= 1024: one launch of 32 x 32
 //    MFMA tiles whose 16 waves split k and meet in LDS (small_mfma_kernel).
 #include <type_traits>
+
+#include <utility>
 
 #include "common.hpp"
 
@@ -217,10 +219,23 @@ __device__ __forceinline__ void store_slice(const float4 (&regs)[CHUNKS], float*
 }
 
 // The same slice copied straight from global memory into LDS (interior
-// slices of f32 operands, 16-byte aligned rows): one global_load_lds_dwordx4
-// fills 64 consecutive 16-byte slots, lane i slot i, so each lane fetches
-// the chunk that belongs in its slot. No registers, no LDS write
+// slices of f32 operands, 16-byte aligned rows): one buffer_load_dwordx4 with
+// the lds bit fills 64 consecutive 16-byte slots, lane i slot i, so each lane
+// fetches the chunk that belongs in its slot. No registers, no LDS write
 // instructions; completion is tracked by vmcnt (wait before the barrier).
+// Buffer loads, not global_load_lds: the compiler counts a pending global
+// (FLAT) load into LDS as a possible LDS access, and then waits for every
+// LDS read at once (lgkmcnt(0)) before each MFMA group, so no operand read
+// could run ahead of the MFMAs (4096^3 985 -> 961-968 us, 2048^3 141 ->
+// 134 us). The buffer is the slice itself, from its first element, so the
+// lane offsets are 32-bit: launch_mfma takes this path only for leading
+// dimensions up to kDmaMaxLd.
+// Word 3 of a raw (unformatted, unswizzled) buffer descriptor on gfx950.
+constexpr int kRawBufferWord3 = 0x00020000;
+// Longest leading dimension (floats) whose 256-row slice stays under 2^31
+// bytes, the reach of a buffer's 32-bit lane offsets.
+constexpr uint64_t kDmaMaxLd = 1ull << 21;
+
 template <int ROWS, int COLS, int WAVES, bool SWZ>
 __device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t ld, uint64_t r0,
                                           uint64_t c0, float* lds, int wave, int lane) {
@@ -237,13 +252,16 @@ __device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t 
     const unsigned pos = static_cast<unsigned>(lane) % kChunksPerRow;
     const unsigned off0 = SWZ ? (pos ^ lr) * 4u : pos * 4u;
     const unsigned off1 = SWZ ? (pos ^ lr ^ 1u) * 4u : pos * 4u;
-    const float* lane_row = g + lr * ld + c0;
+    const float* base = g + r0 * ld + c0;
+    const uint32_t bytes = static_cast<uint32_t>(((ROWS - 1) * ld + COLS) * sizeof(float));
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), kRawBufferWord3);
 #pragma unroll
     for (unsigned j = 0; j < kPerWave; ++j) {
         const unsigned first = (static_cast<unsigned>(wave) * kPerWave + j) * kRowsPerInstr;
         const unsigned off = (SWZ && ((first >> 3) & 1u)) ? off1 : off0;
-        const float* src = lane_row + (r0 + first) * ld + off;
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(lds + first * COLS), 16, 0, 0);
+        const uint32_t voff = static_cast<uint32_t>(((lr + first) * ld + off) * sizeof(float));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + first * COLS), 16, voff, 0, 0, 0);
     }
 }
 
@@ -271,6 +289,24 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_m, uint32_t tiles_n, 
     const uint32_t in_group = id % per_group;
     *tm = first_m + in_group % rows_in_group;
     *tn = in_group / rows_in_group;
+}
+
+// Scheduling of one slice's k steps (4 per group of 8 k): the LDS reads of
+// step s + 2 are placed after the MFMAs of step s, so each step's operands
+// are read a whole step ahead. Read counts per step for A swizzled (one
+// 16-byte read per m block at a group's first step) and B k-major (the
+// step's KNI floats, read in pairs).
+template <int KMI, int KNI>
+constexpr int step_reads(int s) { return (s % 4 == 0 ? KMI : 0) + (KNI + 1) / 2; }
+template <int KMI, int KNI, int... S>
+__device__ __forceinline__ void sched_reads_ahead(std::integer_sequence<int, S...>) {
+    constexpr int kSteps = sizeof...(S);
+    constexpr int kDsRead = 0x100, kMfma = 0x008;
+    __builtin_amdgcn_sched_group_barrier(kDsRead, step_reads<KMI, KNI>(0), 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, step_reads<KMI, KNI>(1), 0);
+    ((__builtin_amdgcn_sched_group_barrier(kMfma, KMI * KNI, 0),
+      __builtin_amdgcn_sched_group_barrier(kDsRead, S + 2 < kSteps ? step_reads<KMI, KNI>(S + 2) : 0, 0)),
+     ...);
 }
 
 // One tile's product, C[m0 .., n0 ..] summed over k in [k_begin, k_end),
@@ -415,6 +451,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
+        // The 64-tile kernel (k groups, one MFMA per k step) gets its LDS
+        // reads one k step ahead of the MFMAs (1024^3 25.4 -> 24.4 us); the
+        // larger tiles' own schedule was as fast.
+        if constexpr (KG > 1 && kASwz && !kBSwz)
+            sched_reads_ahead<Cfg::kMI, Cfg::kNI>(std::make_integer_sequence<int, BK / 8 / KG * 4>{});
     };
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
@@ -1785,7 +1826,10 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
         return launch_gemv<kGemvMaxRows, BT>(ctx, a, b, out, k, n, addend, addend_mode, m / kGemvMaxRows);
     }
     const uint64_t lda = ta ? m : k, ldb = tb ? k : n;
-    const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned;
+    // Vector loads (and the direct loads into LDS, whose 32-bit offsets need
+    // leading dimensions up to kDmaMaxLd).
+    const bool vec = lda % 4 == 0 && ldb % 4 == 0 && mhip::aligned16(a) && b_aligned &&
+                     lda <= kDmaMaxLd && ldb <= kDmaMaxLd;
     switch (choose_tiles(ctx, m, k, n)) {
         case TileChoice::kTiny:
             if (!ta && !tb)
