@@ -101,42 +101,26 @@ struct PrefillCfg {
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
+// Word 3 of a raw (unformatted, unswizzled) buffer descriptor on gfx950.
+constexpr int kRawBufferWord3 = 0x00020000;
 
 // Rows [k0, k0 + 32) of a row-major [*, W] operand (leading dimension ld)
-// into an LDS tile of 32 x W floats, by direct global -> LDS loads: one
-// instruction fills 1 KB of consecutive 16-byte slots, lane i slot i. Slot
-// (row, c) holds the row's chunk c ^ (row & 15) (XOR swizzle instead of
-// padding: 16-byte reads of one chunk position down 16 rows, which the LDS
-// serves 16 lanes at a time over its 64 banks, and 4-byte reads across a
-// row hit distinct banks). Rows
-// at or past `rows` repeat row rows - 1 (finite data the caller masks out).
-// Completion is tracked by vmcnt: wait for it before the tile's barrier.
-template <int W>
-__device__ __forceinline__ void dma_tile(const float* g, uint64_t ld, uint64_t k0, uint64_t rows,
-                                         float* tile, int wave, int lane) {
-    constexpr int kChunksPerRow = W / 4;
-    constexpr int kInstrPerWave = 32 * W / 4 / 64 / 4;
-    static_assert(kInstrPerWave >= 1 && kChunksPerRow >= 16, "tile must split over four waves");
-#pragma unroll
-    for (int j = 0; j < kInstrPerWave; ++j) {
-        const int slot0 = (wave * kInstrPerWave + j) * 64;
-        const int slot = slot0 + lane;
-        const int row = slot / kChunksPerRow;
-        const int chunk = (slot % kChunksPerRow) ^ (row & 15);
-        uint64_t key = k0 + row;
-        if (k0 + 32 > rows && key >= rows) key = rows - 1;  // only the last tile clamps
-        const float* src = g + key * ld + chunk * 4;
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
-    }
-}
-
-// dma_tile with each lane's byte offsets within a tile (row * ld + its
-// chunk) computed once: a full tile's loads address a uniform base,
-// g + k0 * ld, plus those 32-bit offsets (the global loads' scalar-base
-// form: no per-load address arithmetic). In the last tile, rows at or past
-// `rows` repeat row rows - 1, as in dma_tile. A tile spans 32 * ld * 4
-// bytes, below 2^32 (the launch checks ld).
+// into an LDS tile of 32 x W floats, by direct loads into LDS: one
+// buffer_load_dwordx4 with the lds bit fills 1 KB of consecutive 16-byte
+// slots, lane i slot i. Slot (row, c) holds the row's chunk c ^ (row & 15)
+// (XOR swizzle instead of padding: 16-byte reads of one chunk position down
+// 16 rows, which the LDS serves 16 lanes at a time over its 64 banks, and
+// 4-byte reads across a row hit distinct banks). Rows at or past `rows`
+// repeat row rows - 1 (finite data the caller masks out). Completion is
+// tracked by vmcnt: wait for it before the tile's barrier.
+//
+// Each lane's byte offsets within a tile (row * ld + its chunk) are computed
+// once; a tile's loads address the buffer that starts at g + k0 * ld with
+// those 32-bit offsets. A tile spans 32 * ld * 4 bytes, below 2^32 (the
+// launch checks ld). Buffer loads rather than global_load_lds: the compiler
+// takes a pending global (FLAT) load into LDS for a possible LDS access and
+// then waits for all of a wave's LDS reads at once (1129-1130 -> 1117-1124
+// us at C4, the same bits).
 template <int W>
 struct TileDma {
     static constexpr int kChunksPerRow = W / 4;
@@ -157,13 +141,15 @@ struct TileDma {
 
     __device__ __forceinline__ void load(const float* g, uint64_t ld, uint64_t k0, uint64_t rows,
                                          float* tile, int wave, int lane) const {
-        const char* base = reinterpret_cast<const char*>(g + k0 * ld);
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(g + k0 * ld), 0,
+            static_cast<int>(static_cast<uint32_t>(32 * ld * sizeof(float))), kRawBufferWord3);
         if (k0 + 32 <= rows) {
 #pragma unroll
             for (int j = 0; j < kInstrPerWave; ++j) {
                 const int slot0 = (wave * kInstrPerWave + j) * 64;
-                __builtin_amdgcn_global_load_lds((global_void_t*)(base + off[j]),
-                                                 (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(tile + slot0 * 4), 16, off[j],
+                                                         0, 0, 0);
             }
             return;
         }
@@ -174,8 +160,7 @@ struct TileDma {
             const int slot0 = (wave * kInstrPerWave + j) * 64;
             const uint32_t row = static_cast<uint32_t>(slot0 + lane) / kChunksPerRow;
             const uint32_t o = row > end ? off[j] - (row - end) * row_bytes : off[j];
-            __builtin_amdgcn_global_load_lds((global_void_t*)(base + o),
-                                             (lds_void_t*)(tile + slot0 * 4), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(tile + slot0 * 4), 16, o, 0, 0, 0);
         }
     }
 };
