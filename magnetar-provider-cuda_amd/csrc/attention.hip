@@ -189,6 +189,66 @@ __device__ __forceinline__ v16f tile_scores(const float* sk, const float (&qf)[D
     return s;
 }
 
+// A wave's queries recomputed over their admitted keys only, on the VALU,
+// after its tile loop: taken when an edge tile of the wave held a non-finite
+// V value. In an edge tile a key one query of the wave masks can be one
+// another admits; it enters the P . V MFMA at weight 0 for the first, and a
+// non-finite V there turns that 0 into NaN, where the reference never reads
+// the key (src/kernels.cu:1909-1920). Here each query visits only [lo, hi)
+// (within the workgroup's key chunk), one key at a time: the score from this
+// lane's half of Q^T (qf, pre-scaled to the log2 domain) and the other
+// half's in lane l ^ 32, an online softmax, and this lane's outputs
+// (register r of block vb: column vb*32 + 8*(r/4) + 4*half + r%4), so an
+// admitted inf or NaN gives what the reference's sum gives and a masked one
+// nothing. Slow (each query reads its keys from memory), and only for inputs
+// with non-finite values next to a mask edge; the tile loop's accumulators
+// are dead here, which keeps the kernel within its registers.
+template <int D, int VD>
+__device__ __forceinline__ void recompute_admitted(const float (&qf)[D / 2], const float* K,
+                                                   uint64_t k_ld, const float* V, uint64_t v_ld,
+                                                   uint64_t lo, uint64_t hi, int half,
+                                                   v16f (&o)[VD / 32], float* m_out, float* l_out) {
+#pragma unroll
+    for (int vb = 0; vb < VD / 32; ++vb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[vb][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    for (uint64_t j = lo; j < hi; ++j) {
+        const float* krow = K + j * k_ld + half * (D / 2);
+        float part = 0.0f;
+#pragma unroll
+        for (int t = 0; t < D / 2; t += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(krow + t);
+            part += qf[t] * k4.x + qf[t + 1] * k4.y + qf[t + 2] * k4.z + qf[t + 3] * k4.w;
+        }
+        const float s = part + __shfl_xor(part, 32, 64);
+        const float m_new = fmaxf(m, s);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        const float w = __builtin_amdgcn_exp2f(s - m_use);
+        l = l * alpha + w;
+        const float* vrow = V + j * v_ld;
+#pragma unroll
+        for (int vb = 0; vb < VD / 32; ++vb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 v4 = *reinterpret_cast<const float4*>(vrow + vb * 32 + 8 * g + 4 * half);
+                o[vb][4 * g] = o[vb][4 * g] * alpha + w * v4.x;
+                o[vb][4 * g + 1] = o[vb][4 * g + 1] * alpha + w * v4.y;
+                o[vb][4 * g + 2] = o[vb][4 * g + 2] * alpha + w * v4.z;
+                o[vb][4 * g + 3] = o[vb][4 * g + 3] * alpha + w * v4.w;
+            }
+        m = m_new;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int vb = 0; vb < VD / 32; ++vb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[vb][r] *= inv;
+    *m_out = m;
+    *l_out = l;
+}
+
 // Short prefills, whose query tiles alone would leave most of the device
 // idle, split the key range: chunk c of nchunks covers key tiles [c *
 // chunk_tiles, (c + 1) * chunk_tiles) counted from key 0, and writes, per
@@ -313,6 +373,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
     // The j-th tile walked sits in buffer j & 1 (K and V); the next one is
     // loaded straight into the other buffer while it is used (that buffer
     // held the previous tile, whose readers all passed the previous barrier).
+    bool redo = false;  // an edge tile of this wave held a non-finite V value
     if (i_end > i_begin) {
         load_k(tile_begin + static_cast<uint64_t>(i_begin) * Cfg::kBKV, kbuf(0));
         load_v(tile_begin + static_cast<uint64_t>(i_begin) * Cfg::kBKV, vbuf(0));
@@ -328,11 +389,31 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
             load_v(k0 + Cfg::kBKV, vbuf(cur ^ 1));
         }
         if (wave_in(k0)) {
+            // A tile every query of the wave admits whole needs no mask.
+            const bool masked = !(k0 >= all_lo && k0 + Cfg::kBKV <= all_hi);
+            const float* sv = vbuf(cur);
+            // An edge tile checks its V for non-finite values (integer steps:
+            // an all-ones exponent gives e + 1 = 256, so (e + 1) >> 8 is 1; no
+            // compare masks to hold; four reads in flight), before the scores
+            // while fewer registers are live. One found sends the wave to
+            // recompute_admitted after the loop.
+            if (masked) {
+                uint32_t nonfinite = 0;
+                const mhip::f32x4* tile4 = reinterpret_cast<const mhip::f32x4*>(sv);
+#pragma unroll
+                for (int j = 0; j < Cfg::kVTile / 4 / 64; ++j) {
+                    const mhip::f32x4 v4 = tile4[j * 64 + lane];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        nonfinite |= (((__float_as_uint(v4[e]) >> 23) & 0xFFu) + 1u) >> 8;
+                    if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+                }
+                redo |= __builtin_amdgcn_ballot_w64(nonfinite != 0) != 0;
+            }
             v16f s_cur = tile_scores<D>(kbuf(cur), qf, l32, half);
             // Register r holds key k0 + 8*(r/4) + 4*half + r%4 of query q; bit
-            // j of `admit` says whether tile key j is admitted.
-            // A tile every query of the wave admits whole needs no mask.
-            if (!(k0 >= all_lo && k0 + Cfg::kBKV <= all_hi)) {
+            // j of `span` says whether tile key j is admitted.
+            if (masked) {
                 const int lo_r = min(max(rel_lo - i * Cfg::kBKV, 0), Cfg::kBKV);
                 const int hi_r = min(max(rel_hi - i * Cfg::kBKV, 0), Cfg::kBKV);
                 const uint64_t span = ((1ull << hi_r) - 1ull) & ~((1ull << lo_r) - 1ull);
@@ -365,7 +446,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
             const float keep = (psum == 0.0f && alpha == 1.0f) || l_new == 0.0f ? 1.0f : (l * alpha) * inv;
 #pragma unroll
             for (int r = 0; r < 16; ++r) s_cur[r] *= inv;
-            const float* sv = vbuf(cur);
 #pragma unroll
             for (int vb = 0; vb < VD / 32; ++vb) {
 #pragma unroll
@@ -383,6 +463,14 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnArgs a, Prefil
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    }
+
+    if (redo) {
+        // This workgroup's keys (its tiles [i_begin, i_end)), the query's range within them.
+        const uint64_t c_lo = tile_begin + static_cast<uint64_t>(i_begin) * Cfg::kBKV;
+        const uint64_t c_hi = tile_begin + static_cast<uint64_t>(i_end) * Cfg::kBKV;
+        const uint64_t lo = max(q_lo, c_lo), hi = min(q_hi, c_hi);
+        recompute_admitted<D, VD>(qf, K, k_ld, V, v_ld, lo, hi > lo ? hi : lo, half, o, &m, &l);
     }
 
     // Register r of block vb holds O[q][vb*32 + 8*(r/4) + 4*half + r%4].

@@ -1581,6 +1581,12 @@ mhip_kernel_error mhip_executor_release_step_capture(mhip_executor* ex, const ch
         if (it == ex->captures.end()) return;
         mhip_graph_destroy(it->second.graph);
         ex->captures.erase(it);
+        // Gate buffers outgrown while a capture could read them are freed
+        // once no capture is left, after the replays in flight have ended.
+        if (ex->captures.empty() && !ex->retired_gate_products.empty()) {
+            check(mhip_sync(ex->ctx));
+            ex->retired_gate_products.clear();
+        }
     });
 }
 

@@ -5,7 +5,7 @@
 // Arithmetic: decode both operands exactly to f32, one f32 add or mul, RNE
 // encode -- the reference's kernels (src/kernels.cu:2913-2939) and its exact
 // model (src/tests_conformance.rs:2334-2347); a NaN result's payload follows
-// the x86 rule of the reference CPU Provider (see nan_rule). The codec matches
+// the convention stated at nan_rule. The codec matches
 // src/half_precision.rs:14-125 bit for bit:
 //  - f16 decode uses v_cvt_f32_f16 (exact for every finite value, subnormals
 //    included) and rebuilds NaNs from their bits so a signalling payload is
@@ -72,15 +72,18 @@ __device__ __forceinline__ float materialize(float v) {
     return v;
 }
 
-// A NaN result carries a NaN operand's payload, quieted -- the second
+// A NaN result carries a NaN operand's payload, quieted -- the first
 // operand's when both are NaN; a NaN made from non-NaN operands (inf - inf,
-// 0 * inf) is the negative default quiet NaN. That is what the reference CPU
-// Provider's compiled f32 arithmetic gives on an x86-64 host, stated
-// explicitly (the GPU's ALU would pick a NaN of its own).
+// 0 * inf) is the negative default quiet NaN. This is the convention of the
+// reference CPU Provider's scalar f32 arithmetic as LLVM compiles it for
+// x86-64, stated explicitly (the GPU's ALU would pick a NaN of its own). Which
+// operand survives NaN op NaN is not fixed by the ISA on the reference's side
+// (it follows the compiler's operand order), so only the other rules are
+// pinned bit for bit.
 __device__ __forceinline__ float nan_rule(float x, float y, float r) {
     if (r == r) return r;
-    const uint32_t bits = y != y ? __float_as_uint(y) | 0x00400000u
-                                 : (x != x ? __float_as_uint(x) | 0x00400000u : 0xFFC00000u);
+    const uint32_t bits = x != x ? __float_as_uint(x) | 0x00400000u
+                                 : (y != y ? __float_as_uint(y) | 0x00400000u : 0xFFC00000u);
     return __uint_as_float(bits);
 }
 

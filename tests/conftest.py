@@ -84,3 +84,42 @@ def sweep_seeds(n: int) -> range:
     that is set (a wider sweep on demand; every seed is its own case)."""
     import os
     return range(n * max(1, int(os.environ.get("MHIP_SWEEP_SCALE", "1"))))
+
+
+def is_half_nan(h: np.ndarray, dt: int) -> np.ndarray:
+    """NaN patterns of f16 (dt 0) or bf16 (dt 1) bits."""
+    h = np.asarray(h).astype(np.uint32)
+    if dt == 0:
+        return ((h & 0x7C00) == 0x7C00) & ((h & 0x3FF) != 0)
+    return ((h & 0x7F80) == 0x7F80) & ((h & 0x7F) != 0)
+
+
+def half_nan_candidates(orc, ha: np.ndarray, hb: np.ndarray, dt: int):
+    """The admissible results of NaN op NaN on the half path: either operand's
+    NaN, decoded to f32, quieted (bit 22 set, sign and payload kept) and
+    encoded again. Which of the two survives follows the compiler's operand
+    order on the reference's side, so nothing narrower is pinned."""
+    def quieted(h):
+        f = orc.decode_half(np.ascontiguousarray(h, np.uint16), dt).view(np.uint32)
+        return orc.encode_half((f | np.uint32(0x00400000)).view(np.float32), dt)
+    return quieted(ha), quieted(hb)
+
+
+def assert_half_result(orc, got, want, ha, hb, dt, what: str = "") -> int:
+    """Bit-exact against `want` wherever at least one operand is not NaN; where
+    both are NaN, one of the two admissible quieted payloads. Returns the
+    number of NaN-op-NaN elements checked that way."""
+    got, want = np.asarray(got).reshape(-1), np.asarray(want).reshape(-1)
+    ha, hb = np.asarray(ha).reshape(-1), np.asarray(hb).reshape(-1)
+    both = is_half_nan(ha, dt) & is_half_nan(hb, dt)
+    assert_bitexact(got[~both], want[~both], what)
+    if both.any():
+        ca, cb = half_nan_candidates(orc, ha[both], hb[both], dt)
+        g = got[both]
+        bad = np.nonzero((g != ca) & (g != cb))[0]
+        if len(bad):
+            i = int(bad[0])
+            raise AssertionError(
+                f"{what}: NaN op NaN gave {int(g[i]):#06x}, admissible {int(ca[i]):#06x} "
+                f"or {int(cb[i]):#06x} ({len(bad)} of {g.size} outside the set)")
+    return int(both.sum())

@@ -246,3 +246,62 @@ def test_c4_decode_shape(dev, orc):
         elem = max(elem, max_rel_err_significant(got[b:b + 1], want))
     print(f"C4 decode: worst normwise err {worst:.2e}, elementwise (|ref| >= 1e-3 max) {elem:.2e}")
     assert worst <= TOL
+
+
+def plant_nonfinite(v, d, heads):
+    """V with non-finite values at a few keys: +inf, -inf, NaN, and +inf and
+    -inf in one column of neighbouring keys. Returns the planted copy."""
+    v = v.copy()
+    S = v.shape[0]
+    for h in heads:
+        c = h * d
+        v[min(37, S - 1), c + 5] = np.inf
+        v[min(100, S - 1), c:c + d] = np.nan
+        v[min(130, S - 1), c + 3] = -np.inf
+        v[min(200, S - 2), c + 7] = np.inf
+        v[min(201, S - 1), c + 7] = -np.inf
+        v[S - 1, c + 1] = np.nan
+    return v
+
+
+@pytest.mark.parametrize("S,H,d,window", [(128, 2, 128, None), (256, 2, 128, None),
+                                          (256, 2, 64, None), (256, 2, 128, 16),
+                                          (300, 3, 64, 40), (2048, 32, 128, None)])
+def test_masked_keys_with_non_finite_values_contribute_nothing(dev, orc, S, H, d, window):
+    """Non-finite V rows at keys past some queries' positions (inside those
+    queries' key tiles) and, with a window, before others' first key: a query
+    that does not admit such a key gets the finite result the oracle gives
+    (the reference never reads the key, src/kernels.cu:1909-1920); a query
+    that admits it gets the same non-finite class (inf of the same sign, or
+    NaN) as the oracle's sequential sum. S 128 runs without a key split, 256
+    and 300 with one, 2048 x 32 heads as C4's query tiling; d 64 and 128 are
+    the MFMA prefill's head sizes."""
+    q = orc.normal(S * H * d, 61).reshape(S, H * d)
+    k = orc.normal(S * H * d, 62).reshape(S, H * d)
+    v = orc.normal(S * H * d, 63).reshape(S, H * d)
+    heads = (0, min(2, H))
+    v = plant_nonfinite(v, d, range(H))
+    kw = dict(seq_len=S, kv_rows=S, head_count=H, head_dimension=d, causal=True, window_size=window)
+    got = run(dev, q, k, v, **kw)
+    want = oracle(orc, q, k, v, heads=heads, **kw)
+    cols = slice(heads[0] * d, heads[1] * d)
+    g, w = got[:, cols], want[:, cols]
+    fin = np.isfinite(w)
+    assert (~fin).any() and fin.any()
+    bad = np.nonzero(np.isfinite(g) != fin)
+    assert len(bad[0]) == 0, f"finite pattern differs at (query, col) {list(zip(*bad))[:5]}"
+    assert np.array_equal(np.isnan(g), np.isnan(w))
+    assert np.array_equal(np.signbit(g[np.isinf(w)]), np.signbit(w[np.isinf(w)]))
+    err = float(np.max(np.abs(g[fin] - w[fin]))) / float(np.max(np.abs(w[fin])))
+    print(f"S{S} H{H} d{d} window {window}: {int((~fin).sum())} non-finite outputs, "
+          f"finite ones normwise err {err:.2e}")
+    assert err <= TOL
+    # Queries before the first planted key never see one. A wave (32 queries)
+    # whose edge tile holds a non-finite value recomputes its queries over
+    # their admitted keys on the VALU (another rounding); waves wholly before
+    # the first planted key keep the MFMA path and equal the planted-free run
+    # bit for bit.
+    clean = run(dev, q, k, orc.normal(S * H * d, 63).reshape(S, H * d), **kw)
+    first = min(37, S - 1)
+    assert_bitexact(got[:first // 32 * 32], clean[:first // 32 * 32], "waves before the first key")
+    assert max_normwise_err(got[:first], clean[:first]) <= TOL

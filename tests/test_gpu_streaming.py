@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import assert_bitexact, max_rel_err
+from conftest import assert_bitexact, assert_half_result, is_half_nan, max_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -176,9 +176,10 @@ def test_half_reference_fixtures(dev, orc):
 @pytest.mark.parametrize("op", ["add", "mul"])
 def test_half_random_bit_patterns(dev, orc, dname, op):
     """Uniformly random 16-bit patterns (subnormals, infinities and NaNs
-    included), bit for bit: NaN results too, whose payload follows the
-    reference CPU's x86-64 arithmetic (a NaN operand's, quieted, the second's
-    when both are NaN; the negative default NaN from inf - inf or 0 * inf)."""
+    included), bit for bit: NaN results too (a NaN operand's payload,
+    quieted; the negative default NaN from inf - inf or 0 * inf), except that
+    NaN op NaN may keep either operand's quieted payload, which is all the
+    reference's arithmetic fixes there."""
     dt = HALF[dname]
     rng = np.random.default_rng(11 + dt)
     n = (1 << 22) + 5
@@ -188,19 +189,15 @@ def test_half_random_bit_patterns(dev, orc, dname, op):
     want = orc.half_binary(ha, hb, dt, op)
     nan_w = is_half_nan(want, dt)
     assert nan_w.sum() > 1000  # NaN payloads are exercised
-    assert_bitexact(got, want, f"{op}-{dname}")
+    both = assert_half_result(orc, got, want, ha, hb, dt, f"{op}-{dname}")
+    assert both > 30  # NaN op NaN is exercised (bf16: ~64 of 4M pairs)
+    # This build's convention on top of the admissible set: the first operand's.
+    assert_bitexact(got, want, f"{op}-{dname} (first-operand convention)")
 
 
 def ops_half(dev, ha, hb, op, dt):
     from magnetar_hip import ops
     return ops.half_binary(dev, dev.upload(ha), dev.upload(hb), op, dt).numpy()
-
-
-def is_half_nan(h, dt):
-    h = h.astype(np.uint32)
-    if dt == 0:
-        return ((h & 0x7C00) == 0x7C00) & ((h & 0x3FF) != 0)
-    return ((h & 0x7F80) == 0x7F80) & ((h & 0x7F) != 0)
 
 
 @pytest.mark.parametrize("dname", ["f16", "bf16"])

@@ -49,16 +49,44 @@ def operands(dev, orc, m, k, n, ta, tb, mode, seed):
 
 
 # (m, k, n, transpose_a, transpose_b, addend mode) for each path with scratch.
-GEMV = (1, 4096, 11008, 0, 0, 0)
-GEMV_ROWS = (5, 4096, 1024, 0, 0, 2)
-GEMV_BLOCKS = (16, 512, 1024, 0, 0, 1)
-SPLIT_SMALL = (1024, 1024, 1024, 0, 0, 0)
-SPLIT_BIG = (2048, 2048, 2048, 0, 0, 2)
-STREAM_K = (512, 4096, 11008, 0, 0, 0)
+# Each is checked against mhip_matmul_plan_f32 (test_paths_use_the_scratch),
+# so a change of the time model cannot move a case off the path it is for.
+GEMV = (1, 4096, 11008, 0, 0, 0)          # split-k GEMV
+GEMV_ROWS = (5, 4096, 1024, 0, 0, 2)      # split-k GEMV, 5 rows
+GEMV_BLOCKS = (16, 1100, 512, 0, 0, 1)    # row blocks of 8 (k > 1024: not the small tiles)
+SPLIT_A = (40, 4096, 4096, 0, 0, 0)       # tiles with whole-k splits
+SPLIT_B = (400, 1024, 1900, 0, 0, 2)      # tiles with whole-k splits
+STREAM_K = (512, 4096, 11008, 0, 0, 0)    # stream-K
 TRANSPOSED = (300, 1536, 200, 1, 1, 1)
+NO_SPLIT = (1024, 1024, 1024, 0, 0, 0)    # 64-tiles, no scratch: the array is not used
 
-PAIRS = [(STREAM_K, SPLIT_BIG), (SPLIT_BIG, SPLIT_SMALL), (SPLIT_SMALL, GEMV),
-         (GEMV, GEMV_ROWS), (GEMV_ROWS, GEMV_BLOCKS), (SPLIT_SMALL, TRANSPOSED)]
+PAIRS = [(STREAM_K, SPLIT_A), (SPLIT_A, SPLIT_B), (SPLIT_B, GEMV), (GEMV, GEMV_ROWS),
+         (GEMV_ROWS, GEMV_BLOCKS), (STREAM_K, TRANSPOSED), (SPLIT_A, NO_SPLIT)]
+
+
+def uses_scratch(plan):
+    if plan["path"] in ("gemv", "gemv_row_blocks"):
+        return plan["splits"] > 1
+    return plan["path"] == "tiles" and (plan["splits"] > 1 or plan["stream_k"])
+
+
+def test_paths_use_the_scratch(dev):
+    """Every case above but NO_SPLIT really goes through the scratch array, on
+    the path it is named for."""
+    from magnetar_hip import ops
+    plan = lambda c: ops.matmul_plan(dev, c[0], c[1], c[2], bool(c[3]), bool(c[4]))
+    assert plan(GEMV)["path"] == "gemv" and plan(GEMV)["splits"] > 1, plan(GEMV)
+    assert plan(GEMV_ROWS)["path"] == "gemv" and plan(GEMV_ROWS)["splits"] > 1, plan(GEMV_ROWS)
+    assert plan(GEMV_BLOCKS)["path"] == "gemv_row_blocks", plan(GEMV_BLOCKS)
+    assert plan(GEMV_BLOCKS)["splits"] > 1, plan(GEMV_BLOCKS)
+    for case in (SPLIT_A, SPLIT_B):
+        p = plan(case)
+        assert p["path"] == "tiles" and p["splits"] > 1 and not p["stream_k"], (case, p)
+    assert plan(STREAM_K)["stream_k"], plan(STREAM_K)
+    assert uses_scratch(plan(TRANSPOSED)), plan(TRANSPOSED)
+    assert not uses_scratch(plan(NO_SPLIT)), plan(NO_SPLIT)
+    # Between them the split cases cover more than one tile configuration.
+    assert len({plan(c)["tile"] for c in (SPLIT_A, SPLIT_B, STREAM_K, TRANSPOSED)}) >= 2
 
 
 @pytest.mark.parametrize("first,second", PAIRS)
@@ -103,7 +131,7 @@ def test_a_product_beyond_the_scratch_is_refused(dev, orc):
     assert st == SHAPE_UNSUPPORTED
     assert "bytes of scratch" in dev_detail()
     # The context works on: a product that fits still runs.
-    m2, k2, n2 = SPLIT_SMALL[:3]
+    m2, k2, n2 = SPLIT_A[:3]
     a2 = orc.uniform(m2 * k2, 952, -1.0, 1.0).reshape(m2, k2)
     b2 = orc.uniform(k2 * n2, 953, -1.0, 1.0).reshape(k2, n2)
     st, got = noalloc(dev, dev.upload(a2), dev.upload(b2), m2, k2, n2)
@@ -112,19 +140,30 @@ def test_a_product_beyond_the_scratch_is_refused(dev, orc):
     assert_bitexact(got.numpy(), ops.matmul(dev, dev.upload(a2), dev.upload(b2)).numpy())
 
 
-def test_a_fresh_context_captures_a_split_product_without_allocating(orc):
-    """A new context has no workspace yet: inside a capture the ordinary entry
-    point would have to grow it (refused while capturing), the allocation-free
-    one needs nothing. Its graph replays equal the eager result."""
+@pytest.mark.parametrize("case", [SPLIT_A, STREAM_K, GEMV])
+def test_a_fresh_context_captures_a_split_product_without_allocating(orc, case):
+    """A new context has no workspace yet. Inside a capture the ordinary entry
+    point would have to grow it, which capturing refuses; the
+    allocation-free one needs nothing, and its graph replays equal the eager
+    result."""
     import magnetar_hip
     from magnetar_hip import ops
-    m, k, n = SPLIT_SMALL[:3]
+    m, k, n = case[:3]
     a_host = orc.uniform(m * k, 960, -1.0, 1.0).reshape(m, k)
     b_host = orc.uniform(k * n, 961, -1.0, 1.0).reshape(k, n)
     with magnetar_hip.Device(0) as fresh:
+        assert uses_scratch(ops.matmul_plan(fresh, m, k, n)), case
         a, b = fresh.upload(a_host), fresh.upload(b_host)
         out = fresh.empty((m, n))
         fresh.sync()
+        # The ordinary entry point in a capture on this fresh context: refused.
+        fresh.capture_begin()
+        with pytest.raises(magnetar_hip.MagnetarHipError) as refused:
+            ops.matmul(fresh, a, b, out=out)
+        assert refused.value.code == "CaptureUnsupported", refused.value
+        with pytest.raises(magnetar_hip.MagnetarHipError):
+            fresh.capture_end()
+        # The allocation-free one captures.
         fresh.capture_begin()
         st, _ = noalloc(fresh, a, b, m, k, n, out=out)
         assert st == 0, dev_detail()
