@@ -585,14 +585,15 @@ mhip_status launch_prefill(mhip_ctx* ctx, const AttnArgs& a, uint64_t batch) {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         configured = true;
     }
-    hipLaunchKernelGGL((attn_prefill_kernel<D, VD>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), lds, ctx->stream, a, sp);
+    mhip::launch(ctx, (attn_prefill_kernel<D, VD>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                 lds, a, sp);
     mhip_status st = mhip::check_launch("attention (MFMA prefill)");
     if (st != MHIP_OK || sp.nchunks == 1) return st;
     const uint64_t items = rows * a.heads;
     constexpr uint64_t kItems = 256 / (VD / 4);
-    hipLaunchKernelGGL((attn_prefill_combine_kernel<VD>), dim3(static_cast<unsigned>((items + kItems - 1) / kItems)),
-                       dim3(256), 0, ctx->stream, a, rows, sp);
+    mhip::launch(ctx, (attn_prefill_combine_kernel<VD>),
+                 dim3(static_cast<unsigned>((items + kItems - 1) / kItems)), dim3(256), 0, a, rows,
+                 sp);
     return mhip::check_launch("attention (prefill chunk merge)");
 }
 
@@ -809,8 +810,9 @@ mhip_status launch_decode_chunks(mhip_ctx* ctx, const AttnArgs& a, uint64_t batc
     if (st != MHIP_OK) return st;
     float* part_o = part;
     float* part_ml = part + records * D;
-    hipLaunchKernelGGL((attn_decode_partial_kernel<D4, GT, STEPS>), dim3(static_cast<unsigned>(units * chunks)),
-                       dim3(256), 0, ctx->stream, a, lo, chunks, part_o, part_ml);
+    mhip::launch(ctx, (attn_decode_partial_kernel<D4, GT, STEPS>),
+                 dim3(static_cast<unsigned>(units * chunks)), dim3(256), 0, a, lo, chunks, part_o,
+                 part_ml);
     st = mhip::check_launch("attention (decode chunks)");
     if (st != MHIP_OK) return st;
     if (keep) {
@@ -820,8 +822,8 @@ mhip_status launch_decode_chunks(mhip_ctx* ctx, const AttnArgs& a, uint64_t batc
         keep->extra = part + record_floats;
         return MHIP_OK;
     }
-    hipLaunchKernelGGL(attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
-                       dim3(256), 0, ctx->stream, a, chunks, part_o, part_ml);
+    mhip::launch(ctx, attn_decode_combine_kernel<D4>, dim3(static_cast<unsigned>(batch * a.heads)),
+                 dim3(256), 0, a, chunks, part_o, part_ml);
     return mhip::check_launch("attention (decode combine)");
 }
 
@@ -1085,7 +1087,7 @@ extern "C" mhip_status mhip_attention_f32(mhip_ctx* ctx, const float* q, const f
     if (vd > 256) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention value dimension above 256");
     const uint64_t total = batch * p->seq_len * H;
     if (total / 4 >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "attention: too many rows");
-    hipLaunchKernelGGL(attn_generic_kernel, dim3(static_cast<unsigned>((total + 3) / 4)), dim3(256),
-                       0, ctx->stream, a, total);
+    mhip::launch(ctx, attn_generic_kernel, dim3(static_cast<unsigned>((total + 3) / 4)), dim3(256),
+                 0, a, total);
     return mhip::check_launch("attention (generic)");
 }

@@ -5,7 +5,11 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstring>
 #include <string>
+#include <tuple>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "magnetar_hip.h"
@@ -40,13 +44,23 @@ struct mhip_ctx {
     void* fixed_scratch = nullptr;
     size_t fixed_scratch_bytes = 0;
 
-    // Step capture: while `capturing`, launches on the stream are recorded
-    // into a HIP graph instead of running. Launches whose attribute is in
-    // `advancing` (MHIP_ADVANCE_* bits) add the replay offset read from the
-    // device word `offset`; each records how far it may advance in
+    // Step capture: while `capturing`, launches are recorded (kernel, grid,
+    // argument values; mhip::launch) instead of running. Launches whose
+    // attribute is in `advancing` (MHIP_ADVANCE_* bits) add the replay offset
+    // they read through a pointer that is the address of the word
+    // `capture_offset` when recorded; each records how far it may advance in
     // `max_offset`. `failure` keeps the first reason the capture cannot be
     // replayed (an allocation, a transfer, a synchronisation).
     bool capturing = false;
+    struct RecordedLaunch {
+        const void* kernel = nullptr;
+        dim3 grid, block;
+        size_t shmem = 0;
+        std::vector<unsigned char> args;  // argument values, each at its alignment
+        std::vector<size_t> offsets;      // argument i at args[offsets[i]]
+        std::vector<size_t> patches;      // where args holds the offset word's address
+    };
+    std::vector<RecordedLaunch> recorded;
     uint32_t advancing = 0;
     uint64_t* capture_offset = nullptr;
     uint64_t max_offset = 0;
@@ -171,6 +185,52 @@ mhip_status forbid_in_capture(mhip_ctx* ctx, const char* what);
 // stays in bounds for offsets up to `max_offset`. nullptr otherwise (no
 // offset is added).
 const uint64_t* advance_ptr(mhip_ctx* ctx, uint32_t bit, uint64_t max_offset);
+
+// Appends a recorded launch to the capture in progress, noting each 8-byte
+// field of its arguments that holds the capture's offset-word address (an
+// advancing launch's offset pointer) for the replay to redirect.
+void record_launch(mhip_ctx* ctx, mhip_ctx::RecordedLaunch&& launch);
+
+// Every kernel launch of the library goes through here: the arguments are
+// converted to the kernel's parameter types and launched on the context's
+// stream (hipLaunchKernel with the kernel's host handle), or, while a step
+// capture is in progress, recorded with their values for mhip_graph_launch
+// to re-issue. The launch's error is left for check_launch, as with a plain
+// launch.
+template <typename... P, typename... A>
+void launch(mhip_ctx* ctx, void (*kernel)(P...), dim3 grid, dim3 block, size_t shmem, A&&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "a kernel argument is missing or extra");
+    std::tuple<std::decay_t<P>...> values(std::forward<A>(args)...);
+    if (ctx->capturing) {
+        mhip_ctx::RecordedLaunch r;
+        r.kernel = reinterpret_cast<const void*>(kernel);
+        r.grid = grid;
+        r.block = block;
+        r.shmem = shmem;
+        std::apply(
+            [&r](const auto&... v) {
+                auto append = [&r](const void* src, size_t size, size_t align) {
+                    const size_t at = (r.args.size() + align - 1) / align * align;
+                    r.args.resize(at + size);
+                    std::memcpy(r.args.data() + at, src, size);
+                    r.offsets.push_back(at);
+                };
+                (append(&v, sizeof(v), alignof(std::decay_t<decltype(v)>)), ...);
+            },
+            values);
+        record_launch(ctx, std::move(r));
+        return;
+    }
+    void* argv[sizeof...(P) > 0 ? sizeof...(P) : 1] = {};
+    std::apply(
+        [&argv](auto&... v) {
+            size_t i = 0;
+            ((argv[i++] = static_cast<void*>(&v)), ...);
+        },
+        values);
+    (void)hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, shmem,
+                          ctx->stream);
+}
 
 // The context's grow-only scratch of at least `bytes` (split-k partials,
 // attention chunk records). Growing it waits for the stream; a buffer a live

@@ -211,11 +211,11 @@ mhip_status launch_binary(mhip_ctx* ctx, const float* a, const float* b, float* 
     if (!a || !b || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, std::string(what) + ": null buffer");
     if (n / 4 >= kMaxElements) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, std::string(what) + ": too many elements");
     if (mhip::aligned16(a) && mhip::aligned16(b) && mhip::aligned16(out)) {
-        hipLaunchKernelGGL(binary_kernel<Op>, dim3(vec_blocks(n)), dim3(kThreads), 0, ctx->stream,
-                           a, b, out, n, op);
+        mhip::launch(ctx, binary_kernel<Op>, dim3(vec_blocks(n)), dim3(kThreads), 0, a, b, out, n,
+                     op);
     } else {
-        hipLaunchKernelGGL(binary_scalar_kernel<Op>, dim3(scalar_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, a, b, out, n, op);
+        mhip::launch(ctx, binary_scalar_kernel<Op>, dim3(scalar_blocks(n)), dim3(kThreads), 0, a, b,
+                     out, n, op);
     }
     return mhip::check_launch(what);
 }
@@ -228,11 +228,10 @@ mhip_status launch_unary(mhip_ctx* ctx, const float* x, float* out, uint64_t n, 
     if (!x || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, std::string(what) + ": null buffer");
     if (n / 4 >= kMaxElements) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, std::string(what) + ": too many elements");
     if (mhip::aligned16(x) && mhip::aligned16(out)) {
-        hipLaunchKernelGGL(unary_kernel<Op>, dim3(vec_blocks(n)), dim3(kThreads), 0, ctx->stream,
-                           x, out, n, op);
+        mhip::launch(ctx, unary_kernel<Op>, dim3(vec_blocks(n)), dim3(kThreads), 0, x, out, n, op);
     } else {
-        hipLaunchKernelGGL(unary_scalar_kernel<Op>, dim3(scalar_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, x, out, n, op);
+        mhip::launch(ctx, unary_scalar_kernel<Op>, dim3(scalar_blocks(n)), dim3(kThreads), 0, x, out,
+                     n, op);
     }
     return mhip::check_launch(what);
 }
@@ -268,11 +267,10 @@ mhip_status mhip_mul_scalar_f32(mhip_ctx* ctx, const float* a, const float* b, f
     if (n == 0) return MHIP_OK;
     if (!a || !b || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "mul: null buffer");
     if (mhip::aligned16(a) && mhip::aligned16(out)) {
-        hipLaunchKernelGGL(mul_scalar_kernel, dim3(vec_blocks(n)), dim3(kThreads), 0, ctx->stream,
-                           a, b, out, n);
+        mhip::launch(ctx, mul_scalar_kernel, dim3(vec_blocks(n)), dim3(kThreads), 0, a, b, out, n);
     } else {
-        hipLaunchKernelGGL(mul_scalar_any_kernel, dim3(scalar_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, a, b, out, n);
+        mhip::launch(ctx, mul_scalar_any_kernel, dim3(scalar_blocks(n)), dim3(kThreads), 0, a, b,
+                     out, n);
     }
     return mhip::check_launch("mul by a scalar");
 }
@@ -288,11 +286,12 @@ mhip_status mhip_bias_add_f32(mhip_ctx* ctx, const float* a, const float* bias, 
     if (!a || !bias || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "add: null buffer");
     if (cols % 4 == 0 && mhip::aligned16(a) && mhip::aligned16(bias) && mhip::aligned16(out)) {
         uint64_t n4 = n / 4;
-        hipLaunchKernelGGL(bias_add_vec_kernel, dim3(static_cast<unsigned>(mhip::ceil_div(n4, kPerBlock))),
-                           dim3(kThreads), 0, ctx->stream, a, bias, out, cols / 4, n4);
+        mhip::launch(ctx, bias_add_vec_kernel,
+                     dim3(static_cast<unsigned>(mhip::ceil_div(n4, kPerBlock))), dim3(kThreads), 0,
+                     a, bias, out, cols / 4, n4);
     } else {
-        hipLaunchKernelGGL(bias_add_scalar_kernel, dim3(scalar_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, a, bias, out, cols, n);
+        mhip::launch(ctx, bias_add_scalar_kernel, dim3(scalar_blocks(n)), dim3(kThreads), 0, a, bias,
+                     out, cols, n);
     }
     return mhip::check_launch("bias add");
 }

@@ -95,21 +95,20 @@ mhip_status embedding_impl(mhip_ctx* ctx, const T* table, uint64_t vocab, uint64
                      mhip::aligned16(out);
     const uint64_t dim4 = dim / 4;
     if (vec && dim4 >= 256 && dim4 % 256 == 0 && num_ids * (dim4 / 256) < (1ull << 31)) {
-        hipLaunchKernelGGL((embedding_block_kernel<T>),
-                           dim3(static_cast<unsigned>(num_ids * (dim4 / 256))), dim3(kThreads), 0,
-                           ctx->stream, table, vocab, dim4, ids, num_ids, out, ctx->flags);
+        mhip::launch(ctx, (embedding_block_kernel<T>),
+                     dim3(static_cast<unsigned>(num_ids * (dim4 / 256))), dim3(kThreads), 0, table,
+                     vocab, dim4, ids, num_ids, out, ctx->flags);
     } else if (vec && dim4 > 256) {
-        hipLaunchKernelGGL((embedding_vec_kernel<256, 4, T>), dim3(static_cast<unsigned>(num_ids)),
-                           dim3(kThreads), 0, ctx->stream, table, vocab, dim4, ids, num_ids, out,
-                           ctx->flags);
+        mhip::launch(ctx, (embedding_vec_kernel<256, 4, T>), dim3(static_cast<unsigned>(num_ids)),
+                     dim3(kThreads), 0, table, vocab, dim4, ids, num_ids, out, ctx->flags);
     } else if (vec) {
-        hipLaunchKernelGGL((embedding_vec_kernel<64, 4, T>),
-                           dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads),
-                           0, ctx->stream, table, vocab, dim4, ids, num_ids, out, ctx->flags);
+        mhip::launch(ctx, (embedding_vec_kernel<64, 4, T>),
+                     dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads), 0,
+                     table, vocab, dim4, ids, num_ids, out, ctx->flags);
     } else {
-        hipLaunchKernelGGL((embedding_scalar_kernel<T>),
-                           dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads),
-                           0, ctx->stream, table, vocab, dim, ids, num_ids, out, ctx->flags);
+        mhip::launch(ctx, (embedding_scalar_kernel<T>),
+                     dim3(static_cast<unsigned>(mhip::ceil_div(num_ids, 4))), dim3(kThreads), 0,
+                     table, vocab, dim, ids, num_ids, out, ctx->flags);
     }
     return mhip::check_launch("embedding lookup");
 }

@@ -222,12 +222,12 @@ template <int DT, int OP>
 void launch_half(mhip_ctx* ctx, const uint16_t* a, const uint16_t* b, uint16_t* out, uint64_t n) {
     if (mhip::aligned16(a) && mhip::aligned16(b) && mhip::aligned16(out)) {
         uint64_t slots = (n + 7) / 8;
-        hipLaunchKernelGGL((half_binary_kernel<DT, OP>),
-                           dim3(static_cast<unsigned>(mhip::ceil_div(slots, kPerBlock))),
-                           dim3(kThreads), 0, ctx->stream, a, b, out, n);
+        mhip::launch(ctx, (half_binary_kernel<DT, OP>),
+                     dim3(static_cast<unsigned>(mhip::ceil_div(slots, kPerBlock))), dim3(kThreads),
+                     0, a, b, out, n);
     } else {
-        hipLaunchKernelGGL((half_binary_scalar_kernel<DT, OP>), dim3(grid_stride_blocks(n)),
-                           dim3(kThreads), 0, ctx->stream, a, b, out, n);
+        mhip::launch(ctx, (half_binary_scalar_kernel<DT, OP>), dim3(grid_stride_blocks(n)),
+                     dim3(kThreads), 0, a, b, out, n);
     }
 }
 
@@ -271,11 +271,11 @@ mhip_status mhip_encode_half(mhip_ctx* ctx, const float* in, uint16_t* out, uint
         return mhip::fail(MHIP_DTYPE_UNSUPPORTED, "half codec takes F16 or BF16");
     if (n == 0) return MHIP_OK;
     if (dtype == MHIP_F16)
-        hipLaunchKernelGGL(encode_kernel<MHIP_F16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, in, out, n);
+        mhip::launch(ctx, encode_kernel<MHIP_F16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
+                     in, out, n);
     else
-        hipLaunchKernelGGL(encode_kernel<MHIP_BF16>, dim3(grid_stride_blocks(n)), dim3(kThreads),
-                           0, ctx->stream, in, out, n);
+        mhip::launch(ctx, encode_kernel<MHIP_BF16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
+                     in, out, n);
     return mhip::check_launch("half encode");
 }
 
@@ -286,11 +286,11 @@ mhip_status mhip_decode_half(mhip_ctx* ctx, const uint16_t* in, float* out, uint
         return mhip::fail(MHIP_DTYPE_UNSUPPORTED, "half codec takes F16 or BF16");
     if (n == 0) return MHIP_OK;
     if (dtype == MHIP_F16)
-        hipLaunchKernelGGL(decode_kernel<MHIP_F16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
-                           ctx->stream, in, out, n);
+        mhip::launch(ctx, decode_kernel<MHIP_F16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
+                     in, out, n);
     else
-        hipLaunchKernelGGL(decode_kernel<MHIP_BF16>, dim3(grid_stride_blocks(n)), dim3(kThreads),
-                           0, ctx->stream, in, out, n);
+        mhip::launch(ctx, decode_kernel<MHIP_BF16>, dim3(grid_stride_blocks(n)), dim3(kThreads), 0,
+                     in, out, n);
     return mhip::check_launch("half decode");
 }
 

@@ -49,12 +49,12 @@ extern "C" mhip_status mhip_kv_write_f32(mhip_ctx* ctx, float* store, uint64_t c
     if (!store || !rows) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "kv-write: null buffer");
     if (n % 4 == 0 && width % 4 == 0 && mhip::aligned16(store) && mhip::aligned16(rows)) {
         const uint64_t n4 = n / 4;
-        hipLaunchKernelGGL(kv_write_vec_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
-                           dim3(256), 0, ctx->stream, reinterpret_cast<const float4*>(rows), store,
-                           width, row_offset, advance, n4);
+        mhip::launch(ctx, kv_write_vec_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
+                     dim3(256), 0, reinterpret_cast<const float4*>(rows), store, width, row_offset,
+                     advance, n4);
     } else {
-        hipLaunchKernelGGL(kv_write_scalar_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-                           dim3(256), 0, ctx->stream, rows, store, width, row_offset, advance, n);
+        mhip::launch(ctx, kv_write_scalar_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
+                     dim3(256), 0, rows, store, width, row_offset, advance, n);
     }
     return mhip::check_launch("kv-write");
 }

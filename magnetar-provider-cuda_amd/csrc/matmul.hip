@@ -818,16 +818,17 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
         if (st != MHIP_OK) return st;
         const dim3 grid(static_cast<unsigned>(plan.groups));
         if (vec)
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>), grid,
-                               dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
+            mhip::launch(ctx,
+                         (mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>),
+                         grid, dim3(Cfg::kThreads), lds, a, b, slot_mem, m, k, n, plan.per);
         else
-            hipLaunchKernelGGL((mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>), grid,
-                               dim3(Cfg::kThreads), lds, ctx->stream, a, b, slot_mem, m, k, n, plan.per);
+            mhip::launch(ctx,
+                         (mfma_gemm_stream_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>),
+                         grid, dim3(Cfg::kThreads), lds, a, b, slot_mem, m, k, n, plan.per);
         st = mhip::check_launch("matmul (MFMA stream-K)");
         if (st != MHIP_OK) return st;
-        hipLaunchKernelGGL((stream_reduce_kernel<BM, BN>), dim3(static_cast<unsigned>(groups_out)),
-                           dim3(256), 0, ctx->stream, slot_mem, c, m, n, plan.kslices, plan.per,
-                           addend, mode, vec4);
+        mhip::launch(ctx, (stream_reduce_kernel<BM, BN>), dim3(static_cast<unsigned>(groups_out)),
+                     dim3(256), 0, slot_mem, c, m, n, plan.kslices, plan.per, addend, mode, vec4);
         return mhip::check_launch("matmul (stream-K reduction)");
     }
 
@@ -838,18 +839,16 @@ mhip_status launch_mfma(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(plan.splits));
     if (vec)
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>), grid,
-                           dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
-                           mode, plan.k_split);
+        mhip::launch(ctx, (mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, true, BT, KG, STEP>), grid,
+                     dim3(Cfg::kThreads), lds, a, b, target, m, k, n, addend, mode, plan.k_split);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>), grid,
-                           dim3(Cfg::kThreads), lds, ctx->stream, a, b, target, m, k, n, addend,
-                           mode, plan.k_split);
+        mhip::launch(ctx, (mfma_gemm_kernel<BM, BN, BK, WM, WN, A_T, B_T, false, BT, KG, STEP>),
+                     grid, dim3(Cfg::kThreads), lds, a, b, target, m, k, n, addend, mode,
+                     plan.k_split);
     mhip_status st = mhip::check_launch("matmul (MFMA tiles)");
     if (st != MHIP_OK || plan.splits == 1) return st;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(groups_out)), dim3(256), 0,
-                       ctx->stream, target, c, m, n, static_cast<uint32_t>(plan.splits), addend, mode,
-                       vec4);
+    mhip::launch(ctx, splitk_reduce_kernel, dim3(static_cast<unsigned>(groups_out)), dim3(256), 0,
+                 target, c, m, n, static_cast<uint32_t>(plan.splits), addend, mode, vec4);
     return mhip::check_launch("matmul (split-k reduction)");
 }
 
@@ -1395,13 +1394,12 @@ void launch_gemv_partial(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, 
                          float* partial, float* c, uint64_t k, uint64_t n, uint64_t k_per_slice,
                          uint64_t slices, const float* addend, int mode) {
     if (stream)
-        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, true, CPL>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices), addend, mode);
+        mhip::launch(ctx, (gemv_partial_kernel<ROWS, BT, true, CPL>), grid, dim3(kGemvThreads), 0, a,
+                     b, partial, c, k, n, k_per_slice, static_cast<uint32_t>(slices), addend, mode);
     else
-        hipLaunchKernelGGL((gemv_partial_kernel<ROWS, BT, false, CPL>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, a, b, partial, c, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices), addend, mode);
+        mhip::launch(ctx, (gemv_partial_kernel<ROWS, BT, false, CPL>), grid, dim3(kGemvThreads), 0,
+                     a, b, partial, c, k, n, k_per_slice, static_cast<uint32_t>(slices), addend,
+                     mode);
 }
 
 // chunk_ss (one row, split k): the output's RMSNorm chunk sums too.
@@ -1436,10 +1434,10 @@ mhip_status launch_gemv(mhip_ctx* ctx, const float* a, const BT* b, float* c, ui
     }
     mhip_status st = mhip::check_launch("matmul (decode partial sums)");
     if (st != MHIP_OK || slices == 1) return st;
-    hipLaunchKernelGGL(gemv_reduce_kernel<ROWS>,
-                       dim3(static_cast<unsigned>(col_groups), 1, static_cast<unsigned>(row_blocks)),
-                       dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
-                       static_cast<uint32_t>(slices), addend, mode, chunk_ss);
+    mhip::launch(ctx, gemv_reduce_kernel<ROWS>,
+                 dim3(static_cast<unsigned>(col_groups), 1, static_cast<unsigned>(row_blocks)),
+                 dim3(kGemvThreads), 0, partial, c, n, static_cast<uint32_t>(slices), addend, mode,
+                 chunk_ss);
     return mhip::check_launch("matmul (decode reduction)");
 }
 
@@ -1447,11 +1445,11 @@ template <int ROWS, class BT, int CPL, int NORM>
 void launch_gemv_set_partial_n(mhip_ctx* ctx, dim3 grid, bool stream, const float* a, uint64_t k,
                                const GemvSet& set, const NormIn& norm) {
     if (stream)
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, true, CPL, NORM>), grid,
-                           dim3(kGemvThreads), 0, ctx->stream, a, k, set, norm);
+        mhip::launch(ctx, (gemv_set_partial_kernel<ROWS, BT, true, CPL, NORM>), grid,
+                     dim3(kGemvThreads), 0, a, k, set, norm);
     else
-        hipLaunchKernelGGL((gemv_set_partial_kernel<ROWS, BT, false, CPL, NORM>), grid,
-                           dim3(kGemvThreads), 0, ctx->stream, a, k, set, norm);
+        mhip::launch(ctx, (gemv_set_partial_kernel<ROWS, BT, false, CPL, NORM>), grid,
+                     dim3(kGemvThreads), 0, a, k, set, norm);
 }
 
 // `norm_mode` (NORM of gemv_set_partial_kernel) is nonzero only for one row.
@@ -1482,8 +1480,8 @@ mhip_status launch_gemv_set(mhip_ctx* ctx, const float* a, uint64_t k, GemvSet s
     }
     mhip_status st = mhip::check_launch("decode projections (partial sums)");
     if (st != MHIP_OK) return st;
-    hipLaunchKernelGGL(gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups, row_blocks),
-                       dim3(kGemvThreads), 0, ctx->stream, set, epilogue, rq, rk);
+    mhip::launch(ctx, gemv_set_reduce_kernel<ROWS>, dim3(reduce_groups, row_blocks),
+                 dim3(kGemvThreads), 0, set, epilogue, rq, rk);
     return mhip::check_launch("decode projections (reduction)");
 }
 
@@ -1688,8 +1686,8 @@ mhip_status launch_small_mfma(mhip_ctx* ctx, const float* a, const BT* b, float*
                               uint64_t k, uint64_t n, const float* addend, int mode) {
     const uint64_t kq = (k + 8 * kSmallWaves - 1) / (8 * kSmallWaves) * 8;
     const dim3 grid(static_cast<unsigned>((n + 31) / 32), static_cast<unsigned>((m + 31) / 32));
-    hipLaunchKernelGGL(small_mfma_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, ctx->stream, a, b, c,
-                       m, k, n, kq, addend, mode);
+    mhip::launch(ctx, small_mfma_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, a, b, c, m, k, n, kq,
+                 addend, mode);
     return mhip::check_launch("matmul (small MFMA tiles)");
 }
 
@@ -1699,8 +1697,8 @@ mhip_status launch_small_set(mhip_ctx* ctx, const float* a, uint64_t rows, uint6
                              const RopeEpi& rk) {
     const uint64_t kq = (k + 8 * kSmallWaves - 1) / (8 * kSmallWaves) * 8;
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>((rows + 31) / 32));
-    hipLaunchKernelGGL(small_mfma_set_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, ctx->stream, a,
-                       rows, k, kq, set, epilogue, rq, rk);
+    mhip::launch(ctx, small_mfma_set_kernel<BT>, grid, dim3(64 * kSmallWaves), 0, a, rows, k, kq,
+                 set, epilogue, rq, rk);
     return mhip::check_launch("GEMV set (small MFMA tiles)");
 }
 
@@ -1804,8 +1802,8 @@ mhip_status matmul_impl(mhip_ctx* ctx, const float* a, const BT* b, float* out, 
     if (m == 0 || n == 0) return MHIP_OK;
     if (!a || !b || !out) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "matmul: null buffer");
     if (k == 0) {
-        hipLaunchKernelGGL(fill_addend_kernel, dim3(static_cast<unsigned>((m * n + 255) / 256)),
-                           dim3(256), 0, ctx->stream, out, m, n, addend, addend_mode);
+        mhip::launch(ctx, fill_addend_kernel, dim3(static_cast<unsigned>((m * n + 255) / 256)),
+                     dim3(256), 0, out, m, n, addend, addend_mode);
         return mhip::check_launch("matmul (empty inner dimension)");
     }
     const bool ta = transpose_a != 0, tb = transpose_b != 0;
@@ -2042,13 +2040,13 @@ void launch_merge_partial(mhip_ctx* ctx, dim3 grid, bool stream, const DecodeChu
                           const BT* b, float* partial, uint64_t k, uint64_t n, uint64_t k_per_slice,
                           uint64_t slices) {
     if (stream)
-        hipLaunchKernelGGL((gemv_partial_merge_kernel<BT, true, CPL, D4>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices));
+        mhip::launch(ctx, (gemv_partial_merge_kernel<BT, true, CPL, D4>), grid, dim3(kGemvThreads),
+                     0, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
+                     static_cast<uint32_t>(slices));
     else
-        hipLaunchKernelGGL((gemv_partial_merge_kernel<BT, false, CPL, D4>), grid, dim3(kGemvThreads), 0,
-                           ctx->stream, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
-                           static_cast<uint32_t>(slices));
+        mhip::launch(ctx, (gemv_partial_merge_kernel<BT, false, CPL, D4>), grid, dim3(kGemvThreads),
+                     0, r.part_o, r.part_ml, r.chunks, b, partial, k, n, k_per_slice,
+                     static_cast<uint32_t>(slices));
 }
 
 template <class BT, int CPL>
@@ -2088,9 +2086,9 @@ mhip_status launch_gemv_merge(mhip_ctx* ctx, const DecodeChunks& r, const BT* b,
     }
     mhip_status st = mhip::check_launch("attention merge + output projection (partial sums)");
     if (st != MHIP_OK) return st;
-    hipLaunchKernelGGL(gemv_reduce_kernel<1>, dim3(static_cast<unsigned>(col_groups), 1, 1),
-                       dim3(kGemvThreads), 0, ctx->stream, partial, c, n,
-                       static_cast<uint32_t>(slices), addend, mode, chunk_ss);
+    mhip::launch(ctx, gemv_reduce_kernel<1>, dim3(static_cast<unsigned>(col_groups), 1, 1),
+                 dim3(kGemvThreads), 0, partial, c, n, static_cast<uint32_t>(slices), addend, mode,
+                 chunk_ss);
     return mhip::check_launch("attention merge + output projection (reduction)");
 }
 

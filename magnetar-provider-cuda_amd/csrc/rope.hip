@@ -288,14 +288,14 @@ mhip_status mhip_rope_f32(mhip_ctx* ctx, const float* in, float* out, uint64_t r
     const bool aligned = mhip::aligned16(in) && mhip::aligned16(out) && cols % 4 == 0 &&
                          head_width % 4 == 0;
     if (aligned && !p.half_split && p.dimension % 4 == 0) {
-        hipLaunchKernelGGL(rope_interleaved_vec_kernel, dim3(static_cast<unsigned>(rows)),
-                           dim3(kThreads), lds, ctx->stream, a);
+        mhip::launch(ctx, rope_interleaved_vec_kernel, dim3(static_cast<unsigned>(rows)),
+                     dim3(kThreads), lds, a);
     } else if (aligned && p.half_split && half % 4 == 0) {
-        hipLaunchKernelGGL(rope_half_split_vec_kernel, dim3(static_cast<unsigned>(rows)),
-                           dim3(kThreads), lds, ctx->stream, a);
+        mhip::launch(ctx, rope_half_split_vec_kernel, dim3(static_cast<unsigned>(rows)),
+                     dim3(kThreads), lds, a);
     } else {
-        hipLaunchKernelGGL(rope_scalar_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                           lds, ctx->stream, a, p.half_split);
+        mhip::launch(ctx, rope_scalar_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), lds,
+                     a, p.half_split);
     }
     return mhip::check_launch("rope");
 }

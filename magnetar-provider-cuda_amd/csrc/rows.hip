@@ -252,17 +252,17 @@ void launch_vec(mhip_ctx* ctx, uint64_t rows, const float* in, const float* weig
     const unsigned blocks = static_cast<unsigned>(mhip::ceil_div(rows, kThreads / G));
     if constexpr (KIND == RowKind::Rms) {
         if (g.bf16)
-            hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT, uint16_t>), dim3(blocks), dim3(kThreads),
-                               0, ctx->stream, reinterpret_cast<const uint16_t*>(in), weight, out,
-                               rows, cols, wstride, eps, g.ids, g.vocab, g.copy, ctx->flags);
+            mhip::launch(ctx, (rmsnorm_vec_kernel<G, VPT, uint16_t>), dim3(blocks), dim3(kThreads),
+                         0, reinterpret_cast<const uint16_t*>(in), weight, out, rows, cols, wstride,
+                         eps, g.ids, g.vocab, g.copy, ctx->flags);
         else
-            hipLaunchKernelGGL((rmsnorm_vec_kernel<G, VPT, float>), dim3(blocks), dim3(kThreads), 0,
-                               ctx->stream, in, weight, out, rows, cols, wstride, eps, g.ids,
-                               g.vocab, g.copy, ctx->flags);
+            mhip::launch(ctx, (rmsnorm_vec_kernel<G, VPT, float>), dim3(blocks), dim3(kThreads), 0,
+                         in, weight, out, rows, cols, wstride, eps, g.ids, g.vocab, g.copy,
+                         ctx->flags);
     }
     else
-        hipLaunchKernelGGL((softmax_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0,
-                           ctx->stream, in, out, rows, cols, ctx->flags);
+        mhip::launch(ctx, (softmax_vec_kernel<G, VPT>), dim3(blocks), dim3(kThreads), 0, in, out,
+                     rows, cols, ctx->flags);
 }
 
 // Picks (G, VPT) for a row of cols4 vectors; returns false when the row
@@ -301,8 +301,8 @@ mhip_status mhip_rmsnorm_f32(mhip_ctx* ctx, const float* in, const float* weight
                      (!weight || mhip::aligned16(weight));
     if (!(vec && dispatch_vec<RowKind::Rms>(ctx, rows, in, weight, out, cols, weight_row_stride,
                                              eps)))
-        hipLaunchKernelGGL(rmsnorm_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                           0, ctx->stream, in, weight, out, cols, weight_row_stride, eps);
+        mhip::launch(ctx, rmsnorm_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                     in, weight, out, cols, weight_row_stride, eps);
     return mhip::check_launch("rmsnorm");
 }
 
@@ -319,8 +319,8 @@ mhip_status mhip_softmax_rows_f32(mhip_ctx* ctx, const float* in, float* out, ui
     if (rows >= (1ULL << 31)) return mhip::fail(MHIP_SHAPE_UNSUPPORTED, "softmax: too many rows");
     const bool vec = cols % 4 == 0 && mhip::aligned16(in) && mhip::aligned16(out);
     if (!(vec && dispatch_vec<RowKind::Softmax>(ctx, rows, in, nullptr, out, cols, 0, 0.0f)))
-        hipLaunchKernelGGL(softmax_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                           0, ctx->stream, in, out, cols, ctx->flags);
+        mhip::launch(ctx, softmax_loop_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                     in, out, cols, ctx->flags);
     return mhip::check_launch("softmax");
 }
 

@@ -89,25 +89,87 @@ mhip_status workspace(mhip_ctx* ctx, size_t bytes, void** out) {
 
 }  // namespace mhip
 
-// A captured step: the instantiated graph and the device word its advancing
-// launches read the replay offset from.
+// A captured step: its recorded launches, re-issued in order on the
+// context's stream by mhip_graph_launch. An advancing launch read the replay
+// offset through a pointer that was the address of the word `offset` when
+// recorded; a replay at offset t points it at entry t of `table`, a device
+// array holding 0, 1, 2, ..., so nothing is written per replay. Offsets past
+// the table's reach (kTableCap entries) are written into `offset` by one
+// small kernel ahead of the launches instead.
 struct mhip_graph {
     mhip_ctx* ctx = nullptr;
-    hipGraphExec_t exec = nullptr;
+    std::vector<mhip_ctx::RecordedLaunch> launches;
+    std::vector<std::vector<void*>> argv;  // argument pointers into launches[i].args
     uint64_t* offset = nullptr;
     uint64_t max_offset = 0;
-    bool offset_read = false;  // some launch of the step reads `offset`
+    bool offset_read = false;  // some launch of the step reads the offset
+    uint64_t* table = nullptr;
+    uint64_t table_entries = 0;
+    std::vector<uint64_t*> old_tables;  // outgrown; replays in flight may read them
 };
 
 namespace {
 
-// Ahead of every replay of a captured step: its offset word. One launch, not
-// a graph node (no memset node either): the graph holds the step's own work
-// only. The failure flags are left alone: like eager calls, a replay only
-// sets them, and mhip_check_flags clears them when it reports them.
+constexpr uint64_t kTableCap = uint64_t(1) << 22;  // 32 MiB of offsets at most
+
+// A replay's offset beyond the table: written into the offset word on the
+// stream, ahead of the step's launches. The failure flags are left alone:
+// like eager calls, a replay only sets them, and mhip_check_flags clears
+// them when it reports them.
 __global__ void replay_offset_kernel(uint64_t* word, uint64_t value) { *word = value; }
 
+// table[i] = first + i for i < n.
+__global__ void iota_kernel(uint64_t* table, uint64_t first, uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) table[i] = first + i;
+}
+
+// Grows the graph's offset table to cover `offset` (doubling, up to
+// kTableCap entries); the old table is kept until the graph goes.
+mhip_status cover_offset(mhip_graph* g, uint64_t offset) {
+    if (offset < g->table_entries) return MHIP_OK;
+    uint64_t entries = std::max<uint64_t>(4096, g->table_entries * 2);
+    while (entries <= offset) entries *= 2;
+    entries = std::min(entries, kTableCap);
+    uint64_t* table = nullptr;
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&table), entries * sizeof(uint64_t));
+    if (err != hipSuccess) return mhip::from_hip(err, "allocating a replay offset table");
+    mhip::launch(g->ctx, iota_kernel, dim3(static_cast<unsigned>((entries + 255) / 256)), dim3(256), 0,
+                 table, uint64_t(0), entries);
+    if (mhip_status st = mhip::check_launch("filling a replay offset table"); st != MHIP_OK) {
+        (void)hipFree(table);
+        return st;
+    }
+    if (g->table) g->old_tables.push_back(g->table);
+    g->table = table;
+    g->table_entries = entries;
+    return MHIP_OK;
+}
+
 }  // namespace
+
+namespace mhip {
+
+void record_launch(mhip_ctx* ctx, mhip_ctx::RecordedLaunch&& launch) {
+    // Pointers sit at 8-byte offsets within an argument aligned to 8; the
+    // offset word's address in any of them is an advancing launch's offset
+    // pointer (a padding byte pattern equal to a live device address would
+    // only be rewritten harmlessly).
+    const uint64_t word = reinterpret_cast<uintptr_t>(ctx->capture_offset);
+    for (size_t i = 0; i < launch.offsets.size(); ++i) {
+        const size_t begin = launch.offsets[i];
+        const size_t end = i + 1 < launch.offsets.size() ? launch.offsets[i + 1] : launch.args.size();
+        if (begin % 8 != 0) continue;
+        for (size_t at = begin; at + 8 <= end; at += 8) {
+            uint64_t v;
+            std::memcpy(&v, launch.args.data() + at, 8);
+            if (v == word) launch.patches.push_back(at);
+        }
+    }
+    ctx->recorded.push_back(std::move(launch));
+}
+
+}  // namespace mhip
 
 extern "C" {
 
@@ -338,19 +400,29 @@ mhip_status mhip_timer_stop(mhip_ctx* ctx, float* elapsed_ms) {
 }
 
 // ---- step capture (src/kernels.rs:1019-1349) ----
+//
+// A captured step is the list of its launches (kernel, grid, argument
+// values), recorded by mhip::launch while capturing and re-issued in order on
+// the stream by mhip_graph_launch. HIP graphs were used first: a
+// hipGraphLaunch of the same launches ran 4.6-7 us slower than issuing them
+// on the stream (the C1 block's seven launches 43.3 vs 38.6 us, the C5
+// decode step 171.4 vs 164.5 us including a kernel writing the offset word),
+// with or without the runtime's graph packet capture. Re-issued launches run
+// exactly as eager ones, and each copies its argument values when issued,
+// so a replay queued behind another never sees the next one's offset.
 
 mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing) {
     MHIP_REQUIRE_CTX(ctx);
     if (ctx->capturing)
         return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "a step capture is already in progress");
     (void)hipSetDevice(ctx->device);
-    // Allocated and zeroed before the capture starts: nothing allocates while
-    // capturing.
+    // The word whose address advancing launches record (and that offsets past
+    // a replay's table are written into); allocated before capturing, since
+    // nothing allocates while capturing.
     uint64_t* offset = nullptr;
     hipError_t err = hipMalloc(reinterpret_cast<void**>(&offset), 256);
     if (err == hipSuccess) err = hipMemset(offset, 0, 256);
-    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
-    if (err == hipSuccess) err = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+    if (err == hipSuccess) err = hipDeviceSynchronize();
     if (err != hipSuccess) {
         if (offset) (void)hipFree(offset);
         return mhip::from_hip(err, "beginning a step capture");
@@ -361,45 +433,40 @@ mhip_status mhip_capture_begin(mhip_ctx* ctx, uint32_t advancing) {
     ctx->max_offset = UINT64_MAX;
     ctx->offset_read = false;
     ctx->capture_failure.clear();
+    ctx->recorded.clear();
     return MHIP_OK;
 }
 
-// Ends capture mode on the stream; returns the captured graph (or null).
-static hipGraph_t stop_capture(mhip_ctx* ctx) {
-    hipGraph_t graph = nullptr;
-    (void)hipStreamEndCapture(ctx->stream, &graph);
-    (void)hipGetLastError();
+// Ends capture mode; the recorded launches stay in ctx->recorded.
+static void stop_capture(mhip_ctx* ctx) {
     ctx->capturing = false;
     for (void* p : ctx->deferred_frees) (void)hipFree(p);
     ctx->deferred_frees.clear();
-    return graph;
 }
 
 mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offset) {
     MHIP_REQUIRE_CTX(ctx);
     if (out) *out = nullptr;
     if (!ctx->capturing) return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "no step capture is in progress");
-    hipGraph_t graph = stop_capture(ctx);
+    stop_capture(ctx);
     std::string failure = ctx->capture_failure;
-    size_t nodes = 0;
-    if (failure.empty() && !graph) failure = "the step capture met a driver error";
-    if (failure.empty() && (hipGraphGetNodes(graph, nullptr, &nodes) != hipSuccess || nodes == 0))
-        failure = "the step capture recorded no work";
-    hipGraphExec_t exec = nullptr;
-    if (failure.empty()) {
-        hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-        if (err != hipSuccess) failure = std::string("instantiating the step: ") + hipGetErrorString(err);
-    }
-    if (graph) (void)hipGraphDestroy(graph);
-    if (!failure.empty() || !out) {
-        if (exec) (void)hipGraphExecDestroy(exec);
+    if (failure.empty() && ctx->recorded.empty()) failure = "the step capture recorded no work";
+    if (failure.empty() && !out) failure = "no graph handle";
+    if (!failure.empty()) {
+        ctx->recorded.clear();
         (void)hipFree(ctx->capture_offset);
         ctx->capture_offset = nullptr;
-        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, failure.empty() ? "no graph handle" : failure);
+        return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, failure);
     }
     mhip_graph* g = new mhip_graph();
     g->ctx = ctx;
-    g->exec = exec;
+    g->launches = std::move(ctx->recorded);
+    ctx->recorded.clear();
+    for (auto& l : g->launches) {
+        std::vector<void*> argv;
+        for (size_t at : l.offsets) argv.push_back(l.args.data() + at);
+        g->argv.push_back(std::move(argv));
+    }
     g->offset = ctx->capture_offset;
     g->max_offset = ctx->max_offset;
     g->offset_read = ctx->offset_read;
@@ -413,8 +480,8 @@ mhip_status mhip_capture_end(mhip_ctx* ctx, mhip_graph** out, uint64_t* max_offs
 mhip_status mhip_capture_abort(mhip_ctx* ctx) {
     MHIP_REQUIRE_CTX(ctx);
     if (!ctx->capturing) return MHIP_OK;
-    hipGraph_t graph = stop_capture(ctx);
-    if (graph) (void)hipGraphDestroy(graph);
+    stop_capture(ctx);
+    ctx->recorded.clear();
     if (ctx->capture_offset) (void)hipFree(ctx->capture_offset);
     ctx->capture_offset = nullptr;
     ctx->capture_failure.clear();
@@ -432,15 +499,28 @@ mhip_status mhip_graph_launch(mhip_graph* graph, uint64_t offset) {
         return mhip::fail(MHIP_SHAPE_UNSUPPORTED,
                           "offset " + std::to_string(offset) + " leaves the captured bounds (at most " +
                               std::to_string(graph->max_offset) + ")");
-    // The offset is written by a kernel on the same stream, ahead of the
-    // graph; a step none of whose launches advances (nothing reads the word)
-    // replays without it (C1 block graph 59.6 -> 53 us).
+    // Where the advancing launches read the offset: entry `offset` of the
+    // table, or (past the table's reach) the offset word, written first.
+    uint64_t word = 0;
     if (graph->offset_read) {
-        hipLaunchKernelGGL(replay_offset_kernel, dim3(1), dim3(1), 0, ctx->stream, graph->offset, offset);
-        mhip_status st = mhip::check_launch("writing the replay offset");
-        if (st != MHIP_OK) return st;
+        if (offset < kTableCap) {
+            if (mhip_status st = cover_offset(graph, offset); st != MHIP_OK) return st;
+            word = reinterpret_cast<uintptr_t>(graph->table + offset);
+        } else {
+            mhip::launch(ctx, replay_offset_kernel, dim3(1), dim3(1), 0, graph->offset, offset);
+            if (mhip_status st = mhip::check_launch("writing the replay offset"); st != MHIP_OK)
+                return st;
+            word = reinterpret_cast<uintptr_t>(graph->offset);
+        }
     }
-    return mhip::from_hip(hipGraphLaunch(graph->exec, ctx->stream), "launching a captured step");
+    for (size_t i = 0; i < graph->launches.size(); ++i) {
+        mhip_ctx::RecordedLaunch& l = graph->launches[i];
+        for (size_t at : l.patches) std::memcpy(l.args.data() + at, &word, sizeof(word));
+        hipError_t err = hipLaunchKernel(l.kernel, l.grid, l.block, graph->argv[i].data(), l.shmem,
+                                         ctx->stream);
+        if (err != hipSuccess) return mhip::from_hip(err, "launching a captured step");
+    }
+    return MHIP_OK;
 }
 
 uint64_t mhip_graph_max_offset(const mhip_graph* graph) { return graph ? graph->max_offset : 0; }
@@ -451,8 +531,9 @@ mhip_status mhip_graph_destroy(mhip_graph* graph) {
     if (ctx->capturing)
         return mhip::fail(MHIP_CAPTURE_UNSUPPORTED, "a captured step cannot be released while capturing");
     (void)hipStreamSynchronize(ctx->stream);
-    (void)hipGraphExecDestroy(graph->exec);
     (void)hipFree(graph->offset);
+    if (graph->table) (void)hipFree(graph->table);
+    for (uint64_t* t : graph->old_tables) (void)hipFree(t);
     ctx->live_graphs -= 1;
     if (ctx->live_graphs == 0) {
         for (void* p : ctx->retired) (void)hipFree(p);

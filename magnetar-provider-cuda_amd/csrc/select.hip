@@ -106,9 +106,9 @@ extern "C" mhip_status mhip_greedy_select_f32(mhip_ctx* ctx, const float* logits
     volatile uint64_t* answer = ctx->select_host;
     *answer = ~0ull;
     const uint64_t blocks = std::min<uint64_t>(256, (cols + 4 * kThreads - 1) / (4 * kThreads));
-    hipLaunchKernelGGL(greedy_select_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                       ctx->stream, logits + row * cols, cols, ranges, range_count, temperature,
-                       reinterpret_cast<unsigned long long*>(ctx->select_state), ctx->select_host);
+    mhip::launch(ctx, greedy_select_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                 logits + row * cols, cols, ranges, range_count, temperature,
+                 reinterpret_cast<unsigned long long*>(ctx->select_state), ctx->select_host);
     mhip_status st = mhip::check_launch("greedy selection");
     if (st != MHIP_OK) return st;
     const hipError_t err = hipStreamSynchronize(ctx->stream);

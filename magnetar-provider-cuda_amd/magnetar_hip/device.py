@@ -168,7 +168,7 @@ ADVANCE_POSITION_OFFSET, ADVANCE_KEY_COUNT, ADVANCE_ROW_OFFSET = 1, 2, 4
 
 
 class CapturedStep:
-    """A captured launch sequence (HIP graph); launch(offset) replays it with
+    """A captured launch sequence; launch(offset) re-issues it on the stream with
     every advancing attribute increased by `offset` (at most `max_offset`)."""
 
     def __init__(self, device: Device, handle, max_offset: int):

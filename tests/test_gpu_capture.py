@@ -483,3 +483,47 @@ def test_a_captured_decoder_block_replays_a_prefill_chunk(dev, orc):
         graph.launch(1)
     dev.check_flags()
     graph.close()
+
+
+def test_queued_replays_each_keep_their_own_offset(dev, orc):
+    """A RoPE step (position advancing) and a kv-write step (row advancing),
+    replayed at 64 offsets back to back with no wait between replays: each
+    replay's launches copy their arguments when issued, so every replay
+    writes its own row at its own position, bit for bit the eager RoPE
+    there. The offsets cover the offset table's first size, its growth (5000,
+    100000) and, past its reach (2^22 + 123), the word written ahead of the
+    launches."""
+    from magnetar_hip import ops
+    from magnetar_hip.device import ADVANCE_POSITION_OFFSET, ADVANCE_ROW_OFFSET
+    width, P, capacity = 256, 3, 4096
+    x = orc.normal(width, 91).reshape(1, width)
+    dx = dev.upload(x)
+    offsets = list(range(56)) + [4095, 4000, 5000, 100000, 17, (1 << 22) + 123, 2, 99999]
+    eager = {t: ops.rope(dev, dx, ops.rope_params(64, 4, position_offset=P + t)).numpy()
+             for t in set(offsets)}
+    for t in (0, 100000, (1 << 22) + 123):
+        want, st = orc.rope(x, orc.rope_params(64, 4, position_offset=P + t))
+        assert st == 0 and max_normwise_err(eager[t], want) <= 1e-6
+    y = dev.empty((1, width))
+    store = dev.zeros((P + capacity + 1, width))
+    dev.sync()
+    dev.capture_begin(ADVANCE_POSITION_OFFSET)
+    ops.rope(dev, dx, ops.rope_params(64, 4, position_offset=P), out=y)
+    step_rope = dev.capture_end()
+    dev.capture_begin(ADVANCE_ROW_OFFSET)
+    ops.kv_write(dev, store, y, P)
+    step_row = dev.capture_end()
+    assert step_rope.max_offset >= (1 << 22) + 123
+    assert step_row.max_offset == capacity
+    want_rows = {}
+    for t in offsets:
+        step_rope.launch(t)
+        step_row.launch(t % capacity)  # queued behind the RoPE replay, no wait
+        want_rows[P + t % capacity] = eager[t]  # a later replay of a row wins
+    got = store.numpy()
+    for row, want in want_rows.items():
+        assert np.array_equal(bits(got[row]), bits(want[0])), row
+    untouched = sorted(set(range(P + capacity + 1)) - set(want_rows))
+    assert not np.any(got[untouched])
+    step_rope.close()
+    step_row.close()

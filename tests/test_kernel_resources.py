@@ -68,3 +68,22 @@ def test_no_kernel_uses_scratch():
         assert not offenders, "kernels using scratch:\n" + "\n".join(offenders)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
+
+
+def test_every_launch_goes_through_the_recording_wrapper():
+    """Step capture records the launches made through mhip::launch (common.hpp)
+    and re-issues them on replay; a launch made any other way would run
+    during a capture instead of being recorded. Only the wrapper and the
+    replay itself (runtime.hip) call the HIP launch API."""
+    import glob
+    csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                        "magnetar-provider-cuda_amd", "csrc")
+    found = []
+    for path in sorted(glob.glob(os.path.join(csrc, "*"))):
+        text = open(path).read()
+        name = os.path.basename(path)
+        raw = text.count("hipLaunchKernelGGL") + text.count("<<<") + text.count("hipLaunchKernel(")
+        allowed = {"common.hpp": 1, "runtime.hip": 1}.get(name, 0)
+        if raw != allowed:
+            found.append((name, raw))
+    assert not found, f"launches outside mhip::launch: {found}"
