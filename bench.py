@@ -404,46 +404,96 @@ class CpuLeg:
     workload's count and `data_units` how many the host sample holds; `work`
     is the GPU case's algorithmic bytes or flops per unit and `tokens` its
     tokens per unit. `split`: units are divided over host threads; otherwise
-    one call runs them (`cores` then says how many threads that call uses)."""
+    one call runs them (`cores` then says how many threads that call uses).
+    `single`: a run(r0, r1) for the single-thread figure where `run` itself
+    uses several threads (the C5 prefill block's split products)."""
 
-    def __init__(self, run, units, work, what, data_units=None, tokens=0.0, split=True, cores=1):
+    def __init__(self, run, units, work, what, data_units=None, tokens=0.0, split=True, cores=1,
+                 single=None, single_what=None, single_work=0.0, single_tokens=0.0):
         self.run, self.units, self.work, self.what = run, units, work, what
         self.data_units = data_units or units
         self.tokens, self.split, self.cores = tokens, split, cores
+        self.single, self.single_what = single, single_what
+        self.single_work, self.single_tokens = single_work, single_tokens
+
+
+def _timed_units(run, n, units, runs, pool):
+    """Median seconds of `runs` passes over `units` units split over `n`
+    threads (one call when n is 1), after one untimed pass."""
+    bounds = np.linspace(0, units, n + 1).astype(int)
+
+    def once():
+        if n == 1:
+            run(0, units)
+        else:
+            list(pool.map(lambda i: run(int(bounds[i]), int(bounds[i + 1])), range(n)))
+    once()
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times))
 
 
 def time_cpu_leg(leg, bound, threads, target_s=0.4, runs=3):
+    """The oracle on a bounded sample of the case's workload, two ways
+    on every usable host thread ("value", "cores")
+    and on one thread ("single_thread"). A split leg divides units over
+    threads; a leg that is one sequential call (a GEMV, a decode step, a
+    selection) runs that many independent calls at once for its all-core
+    figure (throughput of concurrent calls over the same data)."""
     from concurrent.futures import ThreadPoolExecutor
     t = time.perf_counter()
     leg.run(0, 1)  # warm-up, and the time of one unit
-    per_unit = time.perf_counter() - t
-    n = min(threads, leg.data_units) if leg.split else 1
-    # Split legs cover at most the host sample; a single-call leg repeats
-    # its call up to the time target.
-    cap = leg.data_units if leg.split else 100000
-    units = int(min(cap, max(n, target_s * n / max(per_unit, 1e-7))))
-    bounds = np.linspace(0, units, n + 1).astype(int)
-    with ThreadPoolExecutor(n) as pool:
-        def once():
-            if n == 1:
-                leg.run(0, units)
+    per_unit = max(time.perf_counter() - t, 1e-7)
+    scale = 1e9 if bound == "hbm" else 1e12
+    unit = "GB/s" if bound == "hbm" else "TFLOP/s"
+
+    def figure(units, sec, cores, sample):
+        out = {"value": round(leg.work * units / sec / scale, 6), "unit": unit, "cores": cores,
+               "sample": sample + f", median of {runs} runs ({sec * 1e3:.1f} ms each) after a warm-up"}
+        if leg.tokens:
+            out["tokens_per_s"] = round(leg.tokens * units / sec, 2)
+        return out
+
+    with ThreadPoolExecutor(max(1, threads)) as pool:
+        if leg.split:
+            n = min(threads, leg.data_units)
+            units = int(min(leg.data_units, max(n, target_s * n / per_unit)))
+            sec = _timed_units(leg.run, n, units, runs, pool)
+            out = figure(units, sec, n, f"{units} of {leg.units} {leg.what} over {n} threads")
+            units1 = int(min(leg.data_units, max(1, target_s / 2 / per_unit)))
+            sec1 = _timed_units(leg.run, 1, units1, runs, pool)
+            out["single_thread"] = figure(units1, sec1, 1, f"{units1} of {leg.units} {leg.what}")
+        else:
+            # One call holds `units` units in sequence.
+            units = int(min(100000, max(1, target_s / per_unit)))
+            if leg.cores > 1:
+                sec = _timed_units(leg.run, 1, units, runs, pool)
+                out = figure(units, sec, leg.cores, f"{units} {leg.what}")
+                if leg.single is not None:
+                    t = time.perf_counter()
+                    leg.single(0, 1)
+                    per1 = max(time.perf_counter() - t, 1e-7)
+                    units1 = int(min(100000, max(1, target_s / 2 / per1)))
+                    sec1 = _timed_units(leg.single, 1, units1, runs, pool)
+                    single = figure(units1, sec1, 1, f"{units1} {leg.single_what}")
+                    single["value"] = round(leg.single_work * units1 / sec1 / scale, 6)
+                    if leg.tokens:
+                        single["tokens_per_s"] = round(leg.single_tokens * units1 / sec1, 2)
+                    out["single_thread"] = single
             else:
-                list(pool.map(lambda i: leg.run(int(bounds[i]), int(bounds[i + 1])), range(n)))
-        once()
-        times = []
-        for _ in range(runs):
-            t = time.perf_counter()
-            once()
-            times.append(time.perf_counter() - t)
-    sec = float(np.median(times))
-    rate = leg.work * units / sec
-    out = {"value": round(rate / (1e9 if bound == "hbm" else 1e12), 6),
-           "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
-           "cores": n if leg.split else leg.cores, "kind": "port",
-           "sample": (f"{units} of {leg.units} {leg.what}" if leg.split else f"{units} {leg.what}")
-                     + f", median of {runs} runs ({sec * 1e3:.1f} ms each) after a warm-up"}
-    if leg.tokens:
-        out["tokens_per_s"] = round(leg.tokens * units / sec, 2)
+                sec1 = _timed_units(leg.run, 1, units, runs, pool)
+                single = figure(units, sec1, 1, f"{units} {leg.what}")
+                n = threads
+                # n independent calls at once, each `units` long.
+                sec = _timed_units(lambda a, b: leg.run(0, units), n, n, runs, pool)
+                out = figure(units * n, sec, n,
+                             f"{n} concurrent calls of {units} {leg.what} (independent, over "
+                             f"the same host data)")
+                out["single_thread"] = single
+    out["kind"] = "port"
     return out
 
 
@@ -553,11 +603,20 @@ def cpu_legs(orc, names):
             ids_p = rng.integers(0, 32000, seq).astype(np.float32)
             zp = np.zeros((seq, 4096), np.float32)
             flops = 2.0 * seq * (4 * 4096 * 4096 + 3 * 4096 * 11008) + 4.0 * 128 * seq * (seq + 1) / 2 * 32
+            seq1 = 8  # the single-thread sample: an 8-token prefill
+            ids_1 = ids_p[:seq1]
+            z1 = np.zeros((seq1, 4096), np.float32)
+            flops1 = (2.0 * seq1 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
+                      + 4.0 * 128 * seq1 * (seq1 + 1) / 2 * 32)
             legs["decoder_c5_prefill512"] = CpuLeg(
                 lambda a, b: [reference_block(orc, big, wb, ids_p, 0, zp, zp, threads=threads)
                               for _ in range(a, b)],
                 1, flops, "block calls of a 64-token prefill (the 512-token call's products "
-                          "split by rows over threads)", tokens=seq, split=False, cores=threads)
+                          "split by rows over threads)", tokens=seq, split=False, cores=threads,
+                single=lambda a, b: [reference_block(orc, big, wb, ids_1, 0, z1, z1, threads=1)
+                                     for _ in range(a, b)],
+                single_what="block calls of an 8-token prefill on one thread",
+                single_work=flops1, single_tokens=seq1)
         kc, vc = normal((2049, 4096), 0.5), normal((2049, 4096), 0.5)
         ids_d = rng.integers(0, 32000, 1).astype(np.float32)
         weight_bytes = 4 * (4 * 4096 * 4096 + 3 * 4096 * 11008)
