@@ -238,7 +238,8 @@ constexpr uint64_t kDmaMaxLd = 1ull << 21;
 
 template <int ROWS, int COLS, int WAVES, bool SWZ>
 __device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t ld, uint64_t r0,
-                                          uint64_t c0, float* lds, int wave, int lane) {
+                                          uint64_t c0, float* lds, int wave, int lane, int part = 0,
+                                          int parts = 1) {
     constexpr unsigned kChunksPerRow = COLS / 4;
     static_assert(64 % kChunksPerRow == 0, "an instruction covers whole rows");
     constexpr unsigned kRowsPerInstr = 64 / kChunksPerRow;
@@ -256,8 +257,9 @@ __device__ __forceinline__ void dma_slice(const float* __restrict__ g, uint64_t 
     const uint32_t bytes = static_cast<uint32_t>(((ROWS - 1) * ld + COLS) * sizeof(float));
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), kRawBufferWord3);
+    const unsigned j0 = kPerWave * part / parts, j1 = kPerWave * (part + 1) / parts;
 #pragma unroll
-    for (unsigned j = 0; j < kPerWave; ++j) {
+    for (unsigned j = j0; j < j1; ++j) {
         const unsigned first = (static_cast<unsigned>(wave) * kPerWave + j) * kRowsPerInstr;
         const unsigned off = (SWZ && ((first >> 3) & 1u)) ? off1 : off0;
         const uint32_t voff = static_cast<uint32_t>(((lr + first) * ld + off) * sizeof(float));
@@ -394,6 +396,24 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         else
             load_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kBChunks, T, VEC>(rb, B, N, k0, n0, k_end, N);
     };
+    // Part `part` of `parts` of a direct slice's loads, issued by a DMA
+    // wave (the caller's branch).
+    auto issue_part_dma = [&](uint64_t k0, int buf, int part, int parts) {
+        float* la = lds + buf * Cfg::kLdsA;
+        float* lb = lds_b0 + buf * Cfg::kLdsB;
+        if constexpr (kBDma) {
+            if constexpr (A_T)
+                dma_slice<Cfg::kARows, Cfg::kACols, kDmaWaves, kASwz>(A, M, k0, m0, la, wave, lane, part, parts);
+            else
+                dma_slice<Cfg::kARows, Cfg::kACols, kDmaWaves, kASwz>(A, K, m0, k0, la, wave, lane, part, parts);
+            if constexpr (B_T)
+                dma_slice<Cfg::kBRows, Cfg::kBCols, kDmaWaves, kBSwz>(
+                    reinterpret_cast<const float*>(B), K, n0, k0, lb, wave, lane, part, parts);
+            else
+                dma_slice<Cfg::kBRows, Cfg::kBCols, kDmaWaves, kBSwz>(
+                    reinterpret_cast<const float*>(B), N, k0, n0, lb, wave, lane, part, parts);
+        }
+    };
     auto finish = [&](uint64_t k0, int buf) {
         const bool dma = direct(k0);
         if (!dma)
@@ -410,12 +430,13 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     // per step. Every fill path and operand orientation uses this order, so
     // they all give the same bits.
     const int hsw = lk ^ chunk_swizzle(lrow);  // rows wm*WM + i*32 + lrow share lrow & 15
-    auto compute = [&](int buf) {
+    auto compute_body = [&](int buf, auto hook) {
         const float* la = lds + buf * Cfg::kLdsA;
         const float* lb = lds_b0 + buf * Cfg::kLdsB;
         constexpr int kGroups = BK / 8 / KG;  // groups of 8 k per wave and slice
 #pragma unroll
         for (int gg = 0; gg < kGroups; ++gg) {
+            hook(gg, kGroups);
             const int g = kg * kGroups + gg;
             mhip::f32x4 a4[Cfg::kMI], b4[Cfg::kNI];
             if constexpr (kASwz) {
@@ -451,11 +472,20 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
-        // The 64-tile kernel (k groups, one MFMA per k step) gets its LDS
-        // reads one k step ahead of the MFMAs (1024^3 25.4 -> 24.4 us); the
-        // larger tiles' own schedule was as fast.
-        if constexpr (KG > 1 && kASwz && !kBSwz)
-            sched_reads_ahead<Cfg::kMI, Cfg::kNI>(std::make_integer_sequence<int, BK / 8 / KG * 4>{});
+    };
+    // The 64-tile kernel (k groups, one MFMA per k step) gets its LDS reads
+    // ahead of the MFMAs (1024^3 25.4 -> 24.4 us); the larger tiles' own
+    // schedule was as fast. N k steps in one scheduling region.
+    constexpr bool kReadAhead = KG > 1 && kASwz && !kBSwz;
+    auto schedule = [&](auto n) {
+        if constexpr (kReadAhead)
+            sched_reads_ahead<Cfg::kMI, Cfg::kNI>(std::make_integer_sequence<int, decltype(n)::value>{});
+    };
+    constexpr int kSliceSteps = BK / 8 / KG * 4;  // k steps per wave and slice
+    auto no_hook = [](int, int) {};
+    auto compute = [&](int buf) {
+        compute_body(buf, no_hook);
+        schedule(std::integral_constant<int, kSliceSteps>{});
     };
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
@@ -465,9 +495,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         // buffered: at step t the DMA waves wait for step t's loads, the
         // barrier publishes them and frees the other buffer set (read in
         // step t - 1), which then takes step t + 1 while step t computes.
+        // (Three sets of three-slice steps, or four of two-slice steps, with
+        // the loads two or three steps ahead, ran 1024^3 at 26.1 and 27.5 us
+        // against 24.0: the barriers per step cost more than load latency.)
         const uint64_t steps = (slices + G - 1) / G;
+        const uint64_t full_steps = slices / G;
+        auto set_of = [&](uint64_t t) { return static_cast<int>(t & 1) * G; };
         auto issue_step = [&](uint64_t t) {
-            const int set = static_cast<int>(t & 1) * G;
+            const int set = set_of(t);
 #pragma unroll
             for (int j = 0; j < G; ++j)
                 if (t * G + j < slices) issue(k_begin + (t * G + j) * BK, set + j);
@@ -476,11 +511,52 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         for (uint64_t t = 0; t < steps; ++t) {
             __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of step t have landed
             step_barrier();
-            if (t + 1 < steps) issue_step(t + 1);
-            const int set = static_cast<int>(t & 1) * G;
+            const int set = set_of(t);
+            const uint64_t tn = t + 1;  // the step whose loads go out now
+            const bool next = tn < steps;
+            const int nset = set_of(tn);
+            if constexpr (kReadAhead) {
+                // Several slices per step, each step in one scheduling region,
+                // so the reads of each slice's first k steps go out during
+                // the previous slice's MFMAs (1024^3 24.3-24.6 -> 23.9-24.1
+                // us). When the next step is whole, its loads go out spread
+                // over this step's k groups, slice j's during slice j (1024^3
+                // 23.9 -> 22.2 us); DMA and other waves then run separate
+                // copies of the step, so neither branches inside it.
+                auto loads_of = [&](int j) {
+                    return [&, j](int gg, int groups) {
+                        issue_part_dma(k_begin + (tn * G + j) * BK, nset + j, gg, groups);
+                    };
+                };
+                auto none = [&](int) { return no_hook; };
+                auto run_step = [&](auto hook) {
 #pragma unroll
-            for (int j = 0; j < G; ++j)
-                if (t * G + j < slices) compute(set + j);
+                    for (int j = 0; j < G; ++j) compute_body(set + j, hook(j));
+                    schedule(std::integral_constant<int, G * kSliceSteps>{});
+                };
+                if (next && tn < full_steps) {
+                    if (wave < kDmaWaves) run_step(loads_of);
+                    else run_step(none);
+                    continue;
+                }
+                if (next) issue_step(tn);
+                if (t < full_steps) {
+                    run_step(none);
+                    continue;
+                }
+#pragma unroll
+                for (int j = 0; j < G; ++j)
+                    if (t * G + j < slices) compute(set + j);
+            } else {
+                // The 8-wave 128 x 128 tiles: the loads in one burst, one
+                // block per slice (their own schedule of whole steps was
+                // slower, 2048^3 134.4 -> 138.5 us, and so was spreading
+                // the loads, 134.5 -> 135.9-141 us in three arrangements).
+                if (next) issue_step(tn);
+#pragma unroll
+                for (int j = 0; j < G; ++j)
+                    if (t * G + j < slices) compute(set + j);
+            }
         }
         __syncthreads();
     } else {
