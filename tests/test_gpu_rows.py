@@ -52,6 +52,27 @@ def test_rmsnorm_shapes(dev, orc, rows, cols, weight_mode):
     assert err <= RMS_TOL
 
 
+@pytest.mark.parametrize("rows,cols,gain", [(2048, 4096, True), (2049, 4096, False),
+                                            (1031, 3000, True), (1100, 2052, True)])
+def test_rmsnorm_many_rows_match_small_batches(dev, orc, rows, cols, gain):
+    """From 1024 rows of 513-1024 vectors on, RMSNorm runs a 1024-thread
+    kernel that takes two rows per workgroup (odd row counts and partial
+    last chunks clamp to the last row and column). Its bits must equal the
+    one-row-per-workgroup kernel's, which batches of fewer rows still take,
+    and the oracle within the bar."""
+    from magnetar_hip import ops
+    x = orc.normal(rows * cols, 46).reshape(rows, cols)
+    w = orc.normal(cols, 47, 1.0, 0.1) if gain else None
+    dw = dev.upload(w) if gain else None
+    whole = ops.rmsnorm(dev, dev.upload(x), dw, 1e-5).numpy()
+    for r0 in range(0, rows, 500):
+        part = ops.rmsnorm(dev, dev.upload(np.ascontiguousarray(x[r0:r0 + 500])), dw, 1e-5).numpy()
+        assert_bitexact(whole[r0:r0 + 500], part)
+    want, st = orc.rmsnorm(x, w, 1e-5)
+    assert st == 0
+    assert max_rel_err(whole, want) <= RMS_TOL
+
+
 def test_rmsnorm_per_head(dev, orc):
     """Per-head normalisation: rows of [rows * heads, head_dim] (src/kernels.rs:4013-4040)."""
     from magnetar_hip import ops
