@@ -575,9 +575,74 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         }
     }
 
-    // k groups: the others' sums meet group 0's in LDS (free after the loop's
-    // last barrier), added in group order; group 0 writes the tile.
-    if constexpr (KG > 1) {
+    // Accumulator r of lane l holds C[8*(r/4) + 4*(l/32) + r%4][l%32] of its
+    // 32x32 block; registers [R0, R1) are written.
+    auto store = [&](auto r0, auto r1) {
+#pragma unroll
+        for (int i = 0; i < Cfg::kMI; ++i) {
+#pragma unroll
+            for (int j = 0; j < Cfg::kNI; ++j) {
+                const uint64_t col = n0 + wn * WN + j * 32 + lrow;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = decltype(r0)::value; r < decltype(r1)::value; ++r) {
+                    const uint64_t row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * lk + (r % 4);
+                    if (row < M) {
+                        float v = acc[i][j][r];
+                        if (addend_mode == 1) v = v + addend[col];
+                        else if (addend_mode >= 2) v = apply_addend(v, addend[row * N + col], addend_mode);
+                        out[(row - out_r0) * ldo + (col - out_c0)] = v;
+                    }
+                }
+            }
+        }
+    };
+    using R0 = std::integral_constant<int, 0>;
+    using R8 = std::integral_constant<int, 8>;
+    using R16 = std::integral_constant<int, 16>;
+
+    if constexpr (KG == 2) {
+        // Two k groups: each finishes half of every block's rows, group 0
+        // registers 0-7 (rows 0-15 of a 32x32 block), group 1 registers
+        // 8-15, handing the other half to its partner through LDS (free
+        // after the loop's last barrier), so both groups add and write. The
+        // sum is group 0's plus group 1's either way.
+        constexpr int kHalf = Cfg::kMI * Cfg::kNI * 8 * 64;  // floats per wave and half
+        float* const given = lds + (kg * Cfg::kTileWaves + wt) * kHalf;
+        const float* const taken = lds + ((1 - kg) * Cfg::kTileWaves + wt) * kHalf;
+        auto give = [&](auto base) {
+#pragma unroll
+            for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                for (int j = 0; j < Cfg::kNI; ++j)
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+                        given[((i * Cfg::kNI + j) * 8 + r) * 64 + lane] = acc[i][j][decltype(base)::value + r];
+        };
+        auto take = [&](auto base, auto first) {
+#pragma unroll
+            for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                for (int j = 0; j < Cfg::kNI; ++j)
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const float a = acc[i][j][decltype(base)::value + r];
+                        const float b = taken[((i * Cfg::kNI + j) * 8 + r) * 64 + lane];
+                        acc[i][j][decltype(base)::value + r] = decltype(first)::value ? a + b : b + a;
+                    }
+        };
+        if (kg == 0) give(R8{});
+        else give(R0{});
+        __syncthreads();
+        if (kg == 0) take(R0{}, std::true_type{});
+        else take(R8{}, std::false_type{});
+        __syncthreads();  // LDS is free again
+        if (kg == 0) store(R0{}, R8{});
+        else store(R8{}, R16{});
+        return;
+    } else if constexpr (KG > 1) {
+        // k groups: the others' sums meet group 0's in LDS (free after the
+        // loop's last barrier), added in group order; group 0 writes the tile.
         constexpr int kPer = Cfg::kMI * Cfg::kNI * 16 * 64;  // floats per wave
         for (int q = 1; q < KG; ++q) {
             if (kg == q) {
@@ -603,26 +668,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
         }
         if (kg != 0) return;
     }
-
-    // Accumulator r of lane l holds C[8*(r/4) + 4*(l/32) + r%4][l%32] of its 32x32 block.
-#pragma unroll
-    for (int i = 0; i < Cfg::kMI; ++i) {
-#pragma unroll
-        for (int j = 0; j < Cfg::kNI; ++j) {
-            const uint64_t col = n0 + wn * WN + j * 32 + lrow;
-            if (col >= N) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint64_t row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * lk + (r % 4);
-                if (row < M) {
-                    float v = acc[i][j][r];
-                    if (addend_mode == 1) v = v + addend[col];
-                    else if (addend_mode >= 2) v = apply_addend(v, addend[row * N + col], addend_mode);
-                    out[(row - out_r0) * ldo + (col - out_c0)] = v;
-                }
-            }
-        }
-    }
+    store(R0{}, R16{});
 }
 
 // One tile per workgroup. blockIdx.y is the k split: the workgroup sums k in
