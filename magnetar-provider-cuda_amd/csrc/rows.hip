@@ -4,9 +4,11 @@
 // thread), reduced across a group of G threads -- one wave64 (G = 64, four
 // rows per workgroup) for rows up to 1024 floats, one four-wave workgroup
 // (G = 256) up to 16384 floats -- with butterfly shuffles inside each wave
-// and one LDS exchange between waves, then written once. Rows that are
-// longer, not a multiple of 4 or not 16-byte aligned take a looped kernel
-// that re-reads the row from cache.
+// and one LDS exchange between waves, then written once. Many RMSNorm rows of
+// 2052-4096 floats take a 1024-thread workgroup per two rows instead, the
+// second row's loads ahead of the first row's reduction, with the same bits.
+// Rows that are longer, not a multiple of 4 or not 16-byte aligned take a
+// looped kernel that re-reads the row from cache.
 //
 // The reference uses one 256-thread block and a shared-memory tree for
 // RMSNorm (src/kernels.cu:1098-1138) and one thread per row for softmax
