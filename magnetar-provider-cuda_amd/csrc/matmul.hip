@@ -316,7 +316,7 @@ __device__ __forceinline__ void sched_reads_ahead(std::integer_sequence<int, S..
 // columns < N, plus the addend when addend_mode is 1 or 2. LDS (`lds`) is
 // free on entry and again on return.
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG = 1,
-          int STEP = 0>
+          int STEP = 0, bool SPREAD = true>
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT* __restrict__ B,
                                           uint64_t M, uint64_t K, uint64_t N, uint64_t m0,
                                           uint64_t n0, uint64_t k_begin, uint64_t k_end,
@@ -490,6 +490,30 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
     constexpr int G = Cfg::kGroup;
+    // One slice per barrier (the 256 x 256 and 128 x 128 tiles): the next
+    // slice's direct loads are issued by every wave, a part at the start of
+    // each of its k groups, between the MFMAs (4096^3 968 -> 942-947 us,
+    // 6144^3 3470 -> 3390 us, 3072^3 480 -> 461 us; the same bits). Issued in
+    // one burst by the older wave of each SIMD, they held that wave ~1,400
+    // cycles per slice before its first MFMA. Not in the stream-K kernel,
+    // where the extra copy of the slice loop spilled registers.
+    constexpr bool kSpread = SPREAD && KG == 1 && G == 1 && kBDma;
+    auto part_all = [&](uint64_t k0, int buf, int part, int parts) {
+        if constexpr (kSpread) {
+            float* la = lds + buf * Cfg::kLdsA;
+            float* lb = lds_b0 + buf * Cfg::kLdsB;
+            if constexpr (A_T)
+                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, M, k0, m0, la, wave, lane, part, parts);
+            else
+                dma_slice<Cfg::kARows, Cfg::kACols, Cfg::kWaves, kASwz>(A, K, m0, k0, la, wave, lane, part, parts);
+            if constexpr (B_T)
+                dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
+                    reinterpret_cast<const float*>(B), K, n0, k0, lb, wave, lane, part, parts);
+            else
+                dma_slice<Cfg::kBRows, Cfg::kBCols, Cfg::kWaves, kBSwz>(
+                    reinterpret_cast<const float*>(B), N, k0, n0, lb, wave, lane, part, parts);
+        }
+    };
     if (G > 1 && kBDma && interior_tile && (k_end - k_begin) % BK == 0) {
         // Every slice goes straight to LDS. Steps of G slices, double-
         // buffered: at step t the DMA waves wait for step t's loads, the
@@ -553,7 +577,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                 // slower, 2048^3 134.4 -> 138.5 us, and so was spreading
                 // the loads, 134.5 -> 135.9-141 us in three arrangements, or
                 // issuing each slice's loads just before the same slice of
-                // this step, 134.2 -> 134.7-135.3 us).
+                // this step, 134.2 -> 134.7-135.3 us; every wave issuing a
+                // part of them at each k group, 134.3-134.5 -> 134.2-134.9).
                 if (next) issue_step(tn);
 #pragma unroll
                 for (int j = 0; j < G; ++j)
@@ -561,6 +586,25 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
             }
         }
         __syncthreads();
+    } else if (kSpread && interior_tile && k_end > k_begin && (k_end - k_begin) % BK == 0) {
+        // Every slice goes straight to LDS, double-buffered, one barrier per
+        // slice: each wave waits for its own loads of slice s + 1 (issued
+        // during slice s), then the barrier publishes them and frees the
+        // buffer slice s was read from.
+        if constexpr (kSpread) {
+            part_all(k_begin, 0, 0, 1);
+            __builtin_amdgcn_s_waitcnt(0);
+            step_barrier();
+            for (uint64_t s = 0; s + 1 < slices; ++s) {
+                const int buf = static_cast<int>(s & 1);
+                const uint64_t k_next = k_begin + (s + 1) * BK;
+                compute_body(buf, [&](int gg, int groups) { part_all(k_next, buf ^ 1, gg, groups); });
+                __builtin_amdgcn_s_waitcnt(0);
+                step_barrier();
+            }
+            compute(static_cast<int>((slices - 1) & 1));
+            __syncthreads();
+        }
     } else {
         issue(k_begin, 0);
         finish(k_begin, 0);
@@ -713,7 +757,7 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>::k
         const uint64_t s1 = min(kslices, s0 + (end - u));
         const uint64_t m0 = t / tiles_n * BM, n0 = t % tiles_n * BN;
         float* slot = slots + (2 * static_cast<uint64_t>(blockIdx.x) + seg) * (BM * BN);
-        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP>(A, B, M, K, N, m0, n0, s0 * BK,
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP, false>(A, B, M, K, N, m0, n0, s0 * BK,
                                                                min(K, s1 * BK), lds, slot, m0, n0,
                                                                BN, nullptr, 0);
         u += s1 - s0;
