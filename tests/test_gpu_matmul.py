@@ -331,6 +331,29 @@ def test_large_tile_path_with_transposed_operands(dev, orc, ta, tb):
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n,waves,splits", [(2000, 1056, 3000, 8, 2), (3200, 512, 3968, 4, 1)])
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+def test_128_tiles_one_slice_per_barrier_with_transposed_operands(dev, orc, m, k, n, waves, splits, ta, tb):
+    """The 128 x 128 tiles in launches of more workgroups than CUs, one slice
+    per barrier, every wave issuing part of the next slice's direct loads: the
+    8-wave tiles with a k split (ragged edges, slices of 544 and 512 k) and the
+    4-wave tiles two to a CU. Stored transposed, the operands give the bits of
+    the untransposed product, whose sampled rows match the oracle."""
+    from magnetar_hip import ops
+    plan = ops.matmul_plan(dev, m, k, n, ta, tb)
+    assert plan["tile"] == (128, 128) and plan["waves"] == waves and plan["splits"] == splits, plan
+    assert not plan["stream_k"], plan
+    a = orc.uniform(m * k, 93, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 94, -1.0, 1.0).reshape(k, n)
+    a_in = np.ascontiguousarray(a.T) if ta else a
+    b_in = np.ascontiguousarray(b.T) if tb else b
+    got = ops.matmul(dev, dev.upload(a_in), dev.upload(b_in), ta, tb).numpy()
+    plain = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
+    for r in np.linspace(0, m - 1, 8).astype(int):
+        assert max_normwise_err(plain[r:r + 1], orc.matmul_rows(a, b, int(r), int(r) + 1)) <= TOL
+
+
 def _offset_view(dev, host):
     """`host` on the device 4 bytes past a 16-byte boundary (and the owner to keep alive)."""
     from magnetar_hip.device import DeviceArray
