@@ -430,14 +430,16 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     // per step. Every fill path and operand orientation uses this order, so
     // they all give the same bits.
     const int hsw = lk ^ chunk_swizzle(lrow);  // rows wm*WM + i*32 + lrow share lrow & 15
-    auto compute_body = [&](int buf, auto hook) {
+    // Groups g0 + [0, count) of one slice (g0 < 0: this wave's k group's
+    // share, kg * count + [0, count)); hook(gg, count) runs before group gg.
+    auto compute_range = [&](int buf, auto hook, auto g0c, auto countc) {
+        constexpr int g0 = decltype(g0c)::value, count = decltype(countc)::value;
         const float* la = lds + buf * Cfg::kLdsA;
         const float* lb = lds_b0 + buf * Cfg::kLdsB;
-        constexpr int kGroups = BK / 8 / KG;  // groups of 8 k per wave and slice
 #pragma unroll
-        for (int gg = 0; gg < kGroups; ++gg) {
-            hook(gg, kGroups);
-            const int g = kg * kGroups + gg;
+        for (int gg = 0; gg < count; ++gg) {
+            hook(gg, count);
+            const int g = (g0 < 0 ? kg * count : g0) + gg;
             mhip::f32x4 a4[Cfg::kMI], b4[Cfg::kNI];
             if constexpr (kASwz) {
 #pragma unroll
@@ -473,6 +475,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
             }
         }
     };
+    constexpr int kGroups = BK / 8 / KG;  // groups of 8 k per wave and slice
+    auto compute_body = [&](int buf, auto hook) {
+        compute_range(buf, hook, std::integral_constant<int, -1>{}, std::integral_constant<int, kGroups>{});
+    };
     // The 64-tile kernel (k groups, one MFMA per k step) gets its LDS reads
     // ahead of the MFMAs (1024^3 25.4 -> 24.4 us); the larger tiles' own
     // schedule was as fast. N k steps in one scheduling region.
@@ -483,9 +489,79 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     };
     constexpr int kSliceSteps = BK / 8 / KG * 4;  // k steps per wave and slice
     auto no_hook = [](int, int) {};
-    auto compute = [&](int buf) {
-        compute_body(buf, no_hook);
-        schedule(std::integral_constant<int, kSliceSteps>{});
+    // Two k groups split a slice's four groups of 8 k unevenly on every
+    // fourth slice from the start of the k range (first of each step):
+    // group 0 (waves 0-3) takes groups 0-2, group 1 group 3; elsewhere 0-1
+    // and 2-3. Group 0's waves are the older wave on each SIMD, which wins
+    // MFMA arbitration and finished its even share ~1,700 cycles per step
+    // before the younger one, which then ran alone (1024^3 21.8-21.9 ->
+    // 21.1-21.3 us; 10 of 16 groups to group 0 was slower, 21.5-21.8; the
+    // uneven slice's place in the step did not matter). Every path of the
+    // kernel follows the same split, so its results stay independent of
+    // operand layout and weight format.
+    constexpr bool kUneven = KG == 2;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    // Slice `s` (from k_begin) by k group `grp` (0 or 1).
+    auto compute_uneven = [&](int buf, auto hook, bool first, auto grp) {
+        if constexpr (decltype(grp)::value == 0) {
+            if (first) compute_range(buf, hook, I0{}, I3{});
+            else compute_range(buf, hook, I0{}, I2{});
+        } else {
+            if (first) compute_range(buf, hook, I3{}, I1{});
+            else compute_range(buf, hook, I2{}, I2{});
+        }
+    };
+    auto compute = [&](int buf, uint64_t s) {
+        if constexpr (kUneven) {
+            // Outside whole steps (edge tiles, a last partial step, compact
+            // B): the same groups in the same order, one group at a time.
+            const bool first = s % 4 == 0;
+            const int g_lo = kg == 0 ? 0 : (first ? 3 : 2);
+            const int g_hi = kg == 0 ? (first ? 3 : 2) : 4;
+            const float* la = lds + buf * Cfg::kLdsA;
+            const float* lb = lds_b0 + buf * Cfg::kLdsB;
+            for (int g = g_lo; g < g_hi; ++g) {
+                mhip::f32x4 a4[Cfg::kMI], b4[Cfg::kNI];
+                if constexpr (kASwz) {
+#pragma unroll
+                    for (int i = 0; i < Cfg::kMI; ++i)
+                        a4[i] = *reinterpret_cast<const mhip::f32x4*>(la + (wm * WM + i * 32 + lrow) * BK +
+                                                                 (((2 * g) ^ hsw) << 2));
+                }
+                if constexpr (kBSwz) {
+#pragma unroll
+                    for (int j = 0; j < Cfg::kNI; ++j)
+                        b4[j] = *reinterpret_cast<const mhip::f32x4*>(lb + (wn * WN + j * 32 + lrow) * BK +
+                                                                 (((2 * g) ^ hsw) << 2));
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 8 * g + 4 * lk + e;
+                    float af[Cfg::kMI], bf[Cfg::kNI];
+#pragma unroll
+                    for (int i = 0; i < Cfg::kMI; ++i) {
+                        if constexpr (kASwz) af[i] = a4[i][e];
+                        else af[i] = la[k * BM + wm * WM + i * 32 + lrow];
+                    }
+#pragma unroll
+                    for (int j = 0; j < Cfg::kNI; ++j) {
+                        if constexpr (kBSwz) bf[j] = b4[j][e];
+                        else bf[j] = lb[k * BN + wn * WN + j * 32 + lrow];
+                    }
+#pragma unroll
+                    for (int i = 0; i < Cfg::kMI; ++i)
+#pragma unroll
+                        for (int j = 0; j < Cfg::kNI; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        } else {
+            compute_body(buf, no_hook);
+            schedule(std::integral_constant<int, kSliceSteps>{});
+        }
     };
 
     const uint64_t slices = (k_end - k_begin + BK - 1) / BK;
@@ -553,24 +629,34 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                     };
                 };
                 auto none = [&](int) { return no_hook; };
-                auto run_step = [&](auto hook) {
+                // A whole step by k group grp (the DMA waves are group 0).
+                auto run_step = [&](auto hook, auto grp) {
+                    if constexpr (kUneven && G % 4 == 0) {
 #pragma unroll
-                    for (int j = 0; j < G; ++j) compute_body(set + j, hook(j));
-                    schedule(std::integral_constant<int, G * kSliceSteps>{});
+                        for (int j = 0; j < G; ++j) compute_uneven(set + j, hook(j), j % 4 == 0, grp);
+                        constexpr int kFirst = decltype(grp)::value == 0 ? 12 : 4;
+                        schedule(std::integral_constant<int, G / 4 * kFirst + (G - G / 4) * 8>{});
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < G; ++j) compute_body(set + j, hook(j));
+                        schedule(std::integral_constant<int, G * kSliceSteps>{});
+                    }
                 };
+                static_assert(!kUneven || kDmaWaves == Cfg::kTileWaves, "the DMA waves are k group 0");
                 if (next && tn < full_steps) {
-                    if (wave < kDmaWaves) run_step(loads_of);
-                    else run_step(none);
+                    if (wave < kDmaWaves) run_step(loads_of, I0{});
+                    else run_step(none, I1{});
                     continue;
                 }
                 if (next) issue_step(tn);
                 if (t < full_steps) {
-                    run_step(none);
+                    if (wave < kDmaWaves) run_step(none, I0{});
+                    else run_step(none, I1{});
                     continue;
                 }
 #pragma unroll
                 for (int j = 0; j < G; ++j)
-                    if (t * G + j < slices) compute(set + j);
+                    if (t * G + j < slices) compute(set + j, t * G + j);
             } else {
                 // The 8-wave 128 x 128 tiles: the loads in one burst, one
                 // block per slice (their own schedule of whole steps was
@@ -582,7 +668,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                 if (next) issue_step(tn);
 #pragma unroll
                 for (int j = 0; j < G; ++j)
-                    if (t * G + j < slices) compute(set + j);
+                    if (t * G + j < slices) compute(set + j, t * G + j);
             }
         }
         __syncthreads();
@@ -602,7 +688,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                 __builtin_amdgcn_s_waitcnt(0);
                 step_barrier();
             }
-            compute(static_cast<int>((slices - 1) & 1));
+            compute(static_cast<int>((slices - 1) & 1), slices - 1);
             __syncthreads();
         }
     } else {
@@ -613,7 +699,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
             const int buf = static_cast<int>(s & 1);
             const uint64_t k_next = k_begin + (s + 1) * BK;
             if (s + 1 < slices) issue(k_next, buf ^ 1);
-            compute(buf);
+            compute(buf, s);
             if (s + 1 < slices) finish(k_next, buf ^ 1);
             __syncthreads();
         }
