@@ -499,7 +499,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     // uneven slice's place in the step did not matter). Every path of the
     // kernel follows the same split, so its results stay independent of
     // operand layout and weight format.
-    constexpr bool kUneven = KG == 2;
+    constexpr bool kUneven = KG == 2 && Cfg::kGroup % 4 == 0;  // steps start every fourth slice
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
