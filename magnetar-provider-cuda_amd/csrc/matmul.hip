@@ -19,10 +19,16 @@
 //    8g + 4h + e (group g, lane half h, step e), so a swizzled row gives a
 //    half's four k values of a group in one 16-byte read, and a k-major row
 //    is read as 32 consecutive words per half-wave; every fill path and
-//    transpose uses this order and gives the same bits. Two
-//    configurations: 256 x 256 tiles of 8 waves
-//    (one per CU) for large products, 128 x 128 of 4 waves (two per CU)
-//    otherwise, picked by a time model. Tiles are ordered so that
+//    transpose uses this order and gives the same bits. Four
+//    configurations, picked by a time model: 256 x 256 tiles of 8 waves
+//    (one per CU) for large products; 128 x 128 of 4 waves (two per CU) or
+//    of 8 waves (one per CU, in steps of two slices when every workgroup
+//    fits on the CUs at once); 64 x 64 of 8 waves in two k groups, in steps
+//    of four slices, for products of about one such tile per CU. With one
+//    slice per barrier every wave issues a part of the next slice's direct
+//    loads at each of its k groups; the stepped kernels spread the older
+//    waves' loads over the step (64 x 64) or issue them in one burst
+//    (128 x 128). Tiles are ordered so that
 //    consecutive tiles share a block row of A and each of the 8 XCDs (own
 //    L2) gets a contiguous band of tiles. When the tiles cannot fill the
 //    device, k is split: over up to 8 workgroups per tile (split-k), or in
