@@ -691,6 +691,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
                 const int buf = static_cast<int>(s & 1);
                 const uint64_t k_next = k_begin + (s + 1) * BK;
                 compute_body(buf, [&](int gg, int groups) { part_all(k_next, buf ^ 1, gg, groups); });
+                // Each k step's LDS reads after the previous step's MFMAs
+                // (A stored [m, k], B stored [k, n]): 3072^3 460 -> 455 us,
+                // 4096^3 and 6144^3 within 0.3 %, the same bits.
+                if constexpr (kASwz && !kBSwz)
+                    sched_reads_ahead<Cfg::kMI, Cfg::kNI>(std::make_integer_sequence<int, kSliceSteps>{});
                 __builtin_amdgcn_s_waitcnt(0);
                 step_barrier();
             }
