@@ -320,7 +320,9 @@ __device__ __forceinline__ void sched_reads_ahead(std::integer_sequence<int, S..
 // One tile's product, C[m0 .., n0 ..] summed over k in [k_begin, k_end),
 // written to out[(row - out_r0) * ldo + (col - out_c0)] for the rows < M and
 // columns < N, plus the addend when addend_mode is 1 or 2. LDS (`lds`) is
-// free on entry and again on return.
+// free on entry and again on return. SPREAD lets the one-slice-per-barrier
+// loop have every wave issue part of the next slice's direct loads (the
+// stream-K kernel turns it off).
 template <int BM, int BN, int BK, int WM, int WN, bool A_T, bool B_T, bool VEC, class BT, int KG = 1,
           int STEP = 0, bool SPREAD = true>
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT* __restrict__ B,
