@@ -579,8 +579,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A, const BT*
     // each of its k groups, between the MFMAs (4096^3 968 -> 942-947 us,
     // 6144^3 3470 -> 3390 us, 3072^3 480 -> 461 us; the same bits). Issued in
     // one burst by the older wave of each SIMD, they held that wave ~1,400
-    // cycles per slice before its first MFMA. Not in the stream-K kernel,
-    // where the extra copy of the slice loop spilled registers.
+    // cycles per slice before its first MFMA. The stream-K kernel spreads
+    // the first part of each run only: a second spread copy spilled.
     constexpr bool kSpread = SPREAD && KG == 1 && G == 1 && kBDma;
     auto part_all = [&](uint64_t k0, int buf, int part, int parts) {
         if constexpr (kSpread) {
@@ -856,17 +856,30 @@ __global__ __launch_bounds__((TileCfg<BM, BN, BK, WM, WN, A_T, B_T, KG, STEP>::k
     const uint64_t tiles_n = (N + BN - 1) / BN;
     const uint64_t kslices = (K + BK - 1) / BK;
     const uint64_t total = (M + BM - 1) / BM * tiles_n * kslices;
-    uint64_t u = static_cast<uint64_t>(blockIdx.x) * per;
-    const uint64_t end = min(total, u + per);
-    for (int seg = 0; seg < 2 && u < end; ++seg) {
-        const uint64_t t = u / kslices, s0 = u % kslices;
-        const uint64_t s1 = min(kslices, s0 + (end - u));
-        const uint64_t m0 = t / tiles_n * BM, n0 = t % tiles_n * BN;
-        float* slot = slots + (2 * static_cast<uint64_t>(blockIdx.x) + seg) * (BM * BN);
-        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP, false>(A, B, M, K, N, m0, n0, s0 * BK,
-                                                               min(K, s1 * BK), lds, slot, m0, n0,
-                                                               BN, nullptr, 0);
-        u += s1 - s0;
+    const uint64_t u0 = static_cast<uint64_t>(blockIdx.x) * per;
+    const uint64_t end = min(total, u0 + per);
+    if (u0 >= end) return;
+    // The run's first part and, when it crosses into the next tile, its
+    // second (k from 0). Only the first spreads its direct loads over the
+    // waves (SPREAD): with both, or with the parts in a loop, the kernel
+    // spilled registers. 1280 x 512 x 3328 60.5 -> 59.5 us, 512 x 4096 x
+    // 11008 356.5 -> 356.0 us, the same bits.
+    const uint64_t t0 = u0 / kslices, a0 = u0 % kslices;
+    const uint64_t b0 = min(kslices, a0 + (end - u0));
+    {
+        const uint64_t m0 = t0 / tiles_n * BM, n0 = t0 % tiles_n * BN;
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP, true>(
+            A, B, M, K, N, m0, n0, a0 * BK, min(K, b0 * BK), lds,
+            slots + (2 * static_cast<uint64_t>(blockIdx.x)) * (BM * BN), m0, n0, BN, nullptr, 0);
+    }
+    const uint64_t u1 = u0 + (b0 - a0);
+    if (u1 < end) {
+        const uint64_t t1 = u1 / kslices;
+        const uint64_t b1 = min(kslices, end - u1);
+        const uint64_t m0 = t1 / tiles_n * BM, n0 = t1 % tiles_n * BN;
+        gemm_tile<BM, BN, BK, WM, WN, A_T, B_T, VEC, BT, KG, STEP, false>(
+            A, B, M, K, N, m0, n0, 0, min(K, b1 * BK), lds,
+            slots + (2 * static_cast<uint64_t>(blockIdx.x) + 1) * (BM * BN), m0, n0, BN, nullptr, 0);
     }
 }
 
