@@ -354,6 +354,27 @@ def test_128_tiles_one_slice_per_barrier_with_transposed_operands(dev, orc, m, k
         assert max_normwise_err(plain[r:r + 1], orc.matmul_rows(a, b, int(r), int(r) + 1)) <= TOL
 
 
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1024, 1056, 1024), (1000, 1000, 1000)])
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+def test_64_tiles_with_transposed_operands(dev, orc, m, k, n, ta, tb):
+    """The 64 x 64 tiles in two k groups, whose split of each slice's groups
+    of 8 k is uneven on every fourth slice: the untransposed product takes
+    whole four-slice steps (a partial last step at k = 1056, edge tiles at
+    1000), the transposed ones slice by slice; every path follows the same
+    split, so the bits match. Sampled rows against the oracle."""
+    from magnetar_hip import ops
+    assert ops.matmul_plan(dev, m, k, n, ta, tb)["tile"] == (64, 64)
+    a = orc.uniform(m * k, 95, -1.0, 1.0).reshape(m, k)
+    b = orc.uniform(k * n, 96, -1.0, 1.0).reshape(k, n)
+    a_in = np.ascontiguousarray(a.T) if ta else a
+    b_in = np.ascontiguousarray(b.T) if tb else b
+    got = ops.matmul(dev, dev.upload(a_in), dev.upload(b_in), ta, tb).numpy()
+    plain = ops.matmul(dev, dev.upload(a), dev.upload(b)).numpy()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
+    for r in np.linspace(0, m - 1, 8).astype(int):
+        assert max_normwise_err(plain[r:r + 1], orc.matmul_rows(a, b, int(r), int(r) + 1)) <= TOL
+
+
 def _offset_view(dev, host):
     """`host` on the device 4 bytes past a 16-byte boundary (and the owner to keep alive)."""
     from magnetar_hip.device import DeviceArray
